@@ -1,0 +1,383 @@
+"""Benchmark of the paged-KV attention path on one MI355X.
+
+Headline (the JSON line's `value`): paged decode attention at the
+Llama-2-7B shape — 32 layers, 32/32 heads, head_dim 128, fp16 KV in a
+16384-page pool of 16-token pages, batch 64 with contexts
+lognormal(median 700) clipped to [16, 4096]. One step is one decode sweep
+over the 32 layers (one launch per layer, each layer with its own q).
+`value` is algorithmic KV bytes moved per second (K and V of every cached
+token once, plus q, out and page ids) with all inputs resident in HBM.
+
+Also measured (the `prefill` and `block_copy` objects): chunked-prefill
+attention with K/V append (16 sequences, prompts U[512, 4096], prefixes
+U[0, 2048], chunk 512) as MFMA utilisation of the fp16 dense peak, and the
+8192-block remap copy as HBM bandwidth.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+METRIC = "paged decode attn KV GB/s & % HBM peak at Llama-7B shape; prefill MFMA util"
+PROFILE_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def fill_random_(t: torch.Tensor, gen: torch.Generator, slab_dim: int = 1) -> None:
+    """N(0,1) fp16 fill, one slice along slab_dim at a time (bounded temp)."""
+    for i in range(t.shape[slab_dim]):
+        s = t.select(slab_dim, i)
+        s.copy_(torch.randn(s.shape, generator=gen, device=t.device, dtype=torch.float32))
+
+
+class LaunchTimer:
+    """HIP events around each launch on the current stream."""
+
+    def __init__(self):
+        self.pairs = []
+
+    def start(self):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        return e
+
+    def stop(self, start):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.append((start, e))
+
+    def mean_ms(self) -> float:
+        torch.cuda.synchronize()
+        return float(np.mean([a.elapsed_time(b) for a, b in self.pairs]))
+
+
+# ------------------------------------------------------------------ decode
+
+
+def bench_decode(args, device):
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+
+    w = workloads.llama2_7b_decode()
+    log(f"decode workload: {w.name}; tokens {int(w.kv_len.sum())}, "
+        f"{w.kv_bytes_per_layer() / 2**30:.3f} GiB per layer")
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    pool = ks.KVPool.allocate(w.num_pages, w.num_layers, w.num_kv_heads, w.page_size, w.head_dim,
+                              device)
+    fill_random_(pool.k, gen)
+    fill_random_(pool.v, gen)
+    indptr, indices = w.csr()
+    table = ks.PageTable(indptr, indices, w.kv_len, device)
+    plan = ks.DecodePlan(w.kv_len, w.num_qo_heads, w.num_kv_heads, device,
+                         part_tokens=args.part_tokens)
+    ws = torch.zeros(max(plan.workspace_bytes(w.head_dim), 1), dtype=torch.uint8, device=device)
+    qs = [torch.randn((w.batch, w.num_qo_heads, w.head_dim), generator=gen, device=device
+                      ).to(torch.float16) for _ in range(w.num_layers)]
+    out = torch.empty_like(qs[0])
+    log(f"plan: {plan.info.num_work} work items x {w.num_qo_heads // plan.info.group_size} "
+        f"head groups, part_tokens {plan.info.part_tokens}, {plan.info.num_merge} merged rows")
+
+    def step(timer=None):
+        for layer in range(w.num_layers):
+            s = timer.start() if timer else None
+            ks.paged_decode(pool, layer, table, qs[layer], plan, out=out, workspace=ws)
+            if timer:
+                timer.stop(s)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    # Per-launch durations from HIP events on the launch stream (separate
+    # pass over the same steps so the events do not perturb the headline).
+    timer = LaunchTimer()
+    for _ in range(args.steps):
+        step(timer)
+    launch_ms = timer.mean_ms()
+
+    bytes_per_layer = w.kv_bytes_per_layer()
+    bytes_per_step = bytes_per_layer * w.num_layers
+    gbs = bytes_per_step * args.steps / elapsed / 1e9
+    achieved = bytes_per_layer / (launch_ms * 1e-3) / 1e9
+    res = {
+        "value": gbs,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "launch_ms": launch_ms,
+        "achieved": achieved,
+        "bytes_per_layer": bytes_per_layer,
+        "workload": w,
+        "plan": plan,
+        "pool": pool,
+        "table": table,
+        "qs": qs,
+    }
+    log(f"decode: {res['ms_per_step']:.3f} ms/step, {gbs:.1f} GB/s whole-step; "
+        f"per launch {launch_ms * 1e3:.1f} us = {achieved:.1f} GB/s "
+        f"({achieved / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
+    return res
+
+
+def check_decode_sample(res, device) -> float:
+    """Max-abs error of a few rows of layer 0 against the CPU oracle."""
+    from oracle import paged_attention_ref as ref
+
+    w, pool = res["workload"], res["pool"]
+    import kunserve_amd as ks
+
+    out = ks.paged_decode(pool, 0, res["table"], res["qs"][0], res["plan"])
+    rows = np.argsort(w.kv_len)[[0, len(w.kv_len) // 2, -1]]
+    indptr, indices = w.csr()
+    used = np.concatenate([indices[indptr[b]:indptr[b + 1]] for b in rows])
+    sel = torch.from_numpy(used.astype(np.int64)).to(device)
+    k = pool.k[:, 0].index_select(0, sel)[:, None].cpu().numpy()
+    v = pool.v[:, 0].index_select(0, sel)[:, None].cpu().numpy()
+    ip = np.concatenate([[0], np.cumsum([indptr[b + 1] - indptr[b] for b in rows])])
+    want = ref.decode_attention(res["qs"][0][torch.from_numpy(rows).to(device)].cpu().numpy(), k,
+                                v, 0, ip, np.arange(len(used)), w.kv_len[rows],
+                                1 / math.sqrt(w.head_dim))
+    got = out[torch.from_numpy(rows).to(device)].float().cpu().numpy()
+    return float(np.max(np.abs(got - want)))
+
+
+def cpu_baseline(res, budget_s: float) -> dict:
+    """The CPU oracle (numpy, fp32 compute on fp16 storage, one thread) on
+    whole layers of the same decode workload, until budget_s has elapsed."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import paged_attention_ref as ref
+
+    w, pool = res["workload"], res["pool"]
+    indptr, indices = w.csr()
+    used = np.unique(indices)
+    remap = np.zeros(w.num_pages, dtype=np.int64)
+    remap[used] = np.arange(used.size)
+    sel = torch.from_numpy(used.astype(np.int64)).to(pool.device)
+    done_bytes, t_total, layers = 0, 0.0, 0
+    with threadpool_limits(limits=1):
+        for layer in range(w.num_layers):
+            k = pool.k[:, layer].index_select(0, sel)[:, None].cpu().numpy()
+            v = pool.v[:, layer].index_select(0, sel)[:, None].cpu().numpy()
+            q = res["qs"][layer].cpu().numpy()
+            t0 = time.perf_counter()
+            ref.decode_attention(q, k, v, 0, indptr, remap[indices], w.kv_len,
+                                 1 / math.sqrt(w.head_dim), dtype=np.float32)
+            t_total += time.perf_counter() - t0
+            done_bytes += res["bytes_per_layer"]
+            layers += 1
+            if t_total >= budget_s:
+                break
+    return {"value": done_bytes / t_total / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{layers} of {w.num_layers} layers of the same decode workload "
+                      f"(all {w.batch} rows), numpy fp32 on fp16 pages, "
+                      f"{t_total:.1f} s of CPU time"}
+
+
+# ----------------------------------------------------------------- prefill
+
+
+def bench_prefill(args, device):
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+
+    w = workloads.chunked_prefill()
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    pool = ks.KVPool.allocate(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device)
+    fill_random_(pool.k, gen)
+    fill_random_(pool.v, gen)
+    steps = []
+    for rows, ql, kv in w.steps():
+        need = (kv + w.page_size - 1) // w.page_size
+        indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+        indices = np.concatenate([w.pages[r][:n] for r, n in zip(rows, need)]).astype(np.int32)
+        q_indptr = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
+        T = int(q_indptr[-1])
+        table = ks.PageTable(indptr, indices, kv, device)
+        qi = torch.from_numpy(q_indptr).to(device)
+        plan = ks.PrefillPlan(q_indptr, kv, device)
+        mk = lambda h: torch.randn((T, h, w.head_dim), generator=gen, device=device).half()
+        steps.append((table, qi, plan, mk(w.num_qo_heads), mk(w.num_kv_heads),
+                      mk(w.num_kv_heads), torch.empty((T, w.num_qo_heads, w.head_dim),
+                                                      dtype=torch.float16, device=device)))
+
+    def run(timer=None):
+        for table, qi, plan, q, k, v, out in steps:
+            ks.append_kv(pool, 0, table, qi, k, v)
+            s = timer.start() if timer else None
+            ks.paged_prefill(pool, 0, table, qi, q, plan, out=out)
+            if timer:
+                timer.stop(s)
+
+    reps = max(1, args.steps // 4)
+    for _ in range(max(1, args.warmup)):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    elapsed = (time.perf_counter() - t0) / reps
+    timer = LaunchTimer()
+    run(timer)
+    attn_ms = timer.mean_ms() * len(steps)
+    flops = w.causal_flops()
+    tflops = flops / (attn_ms * 1e-3) / 1e12
+    log(f"prefill: {len(steps)} chunk steps, {elapsed * 1e3:.3f} ms with append; attention "
+        f"{attn_ms:.3f} ms = {tflops:.1f} TFLOP/s ({tflops / FP16_MFMA_PEAK_TFLOPS * 100:.1f}% "
+        f"of fp16 MFMA peak)")
+    return {"workload": w.name, "causal_tflop": flops / 1e12, "steps": len(steps),
+            "ms_with_append": elapsed * 1e3, "attention_ms": attn_ms, "tflops": tflops,
+            "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS}
+
+
+# -------------------------------------------------------------- block copy
+
+
+def bench_copy(args, device):
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+
+    r = workloads.kv_remap()
+    n_pages = 2 * len(r.src)
+    pool = ks.KVPool.allocate(n_pages, r.num_layers, r.num_kv_heads, r.page_size, r.head_dim,
+                              device)
+    pool.k.fill_(1.0)
+    pool.v.fill_(2.0)
+    src = torch.from_numpy(r.src).to(device)
+    dst = torch.from_numpy(r.dst).to(device)
+    reps = max(2, args.steps // 4)
+    ks.copy_blocks(pool, src, dst)
+    torch.cuda.synchronize()
+    timer = LaunchTimer()
+    for _ in range(reps):
+        s = timer.start()
+        ks.copy_blocks(pool, src, dst)
+        timer.stop(s)
+    ms = timer.mean_ms()
+    gbs = r.copy_bytes() / (ms * 1e-3) / 1e9
+    log(f"block copy: {len(r.src)} blocks of {r.copy_bytes() / 4 / len(r.src) / 2**20:.0f} MiB "
+        f"(K and V), {ms:.3f} ms = {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
+    return {"workload": f"remap copy {len(r.src)} blocks x 2 MiB (K+V)", "ms": ms, "gbs": gbs,
+            "hbm_frac": gbs / HBM_PEAK_GBS}
+
+
+def load_traffic():
+    path = os.path.join(PROFILE_DIR, "paged_decode_llama2_7b_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
+    ap.add_argument("--only", choices=["decode", "prefill", "copy"], default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    import kunserve_amd
+
+    log(f"library {kunserve_amd.library_path()}; device "
+        f"{torch.cuda.get_device_properties(device).name}")
+
+    if args.only == "prefill":
+        print(json.dumps({"prefill": bench_prefill(args, device)}))
+        return
+    if args.only == "copy":
+        print(json.dumps({"block_copy": bench_copy(args, device)}))
+        return
+
+    dec = bench_decode(args, device)
+    err = check_decode_sample(dec, device)
+    log(f"decode sample max-abs error vs oracle: {err:.2e}")
+    if err > 2e-3:
+        print(f"decode result check failed: max-abs {err}", file=sys.stderr)
+        sys.exit(1)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(dec, args.cpu_budget)
+        log(f"cpu baseline: {cpu['value']:.3f} GB/s ({cpu['sample']})")
+    w = dec["workload"]
+    del dec["pool"], dec["qs"]
+    torch.cuda.empty_cache()
+    prefill = copy = None
+    if args.only is None:
+        prefill = bench_prefill(args, device)
+        torch.cuda.empty_cache()
+        copy = bench_copy(args, device)
+        torch.cuda.empty_cache()
+
+    line = {
+        "metric": METRIC,
+        "value": round(dec["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": w.name,
+            "layers": w.num_layers, "batch": w.batch, "num_qo_heads": w.num_qo_heads,
+            "num_kv_heads": w.num_kv_heads, "head_dim": w.head_dim, "page_size": w.page_size,
+            "num_pages": w.num_pages, "total_kv_tokens": int(w.kv_len.sum()),
+            "part_tokens": dec["plan"].info.part_tokens,
+            "hbm_frac": round(dec["value"] / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(dec["achieved"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dec["achieved"] / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic(),
+            "kernel": "paged_decode (partition kernel + merge kernel) per layer",
+            "algorithmic_bytes_per_launch": dec["bytes_per_layer"],
+            "launch_us": round(dec["launch_ms"] * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+        "prefill": prefill,
+        "block_copy": copy,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,230 @@
+/*
+ * kunserve_hip.h — C ABI of the MI355X (gfx950) paged-KV attention path.
+ *
+ * This library replaces the GPU side of the KV-cache operators that the
+ * KunServe host layer reaches through libflash_pybinding.so:
+ *
+ *   torch.ops.swapping_ops.swap            kunserve/worker.py:673-681
+ *   LlamaOp.local_copy_blocks              kunserve/worker.py:818-823
+ *   LlamaOp.kv_exchange (pack / scatter)   kunserve/worker.py:514-532,
+ *                                          kunserve/flash_backend.py:857-1022
+ *   LlamaOp.pforward, attention stage      kunserve/worker.py:298-312
+ *       (K/V append into pages, paged decode attention for q_len == 1 rows,
+ *        chunked-prefill causal attention for prefill rows)
+ *
+ * Conventions
+ *   - Every function returns 0 on success and a negative KUNSERVE_E* code on
+ *     failure; kunserve_last_error() returns a message for the calling thread.
+ *   - Pointers named *_dev are device pointers, *_host are host pointers.
+ *   - All device work is enqueued on the given stream; no function
+ *     synchronises the device or the stream, and no function allocates
+ *     device memory: scratch space is passed in by the caller.
+ *   - KV data is fp16. Element (page, layer, kv_head, slot, dim) of the K (or
+ *     V) pool lives at
+ *        page*page_stride + layer*layer_stride + kv_head*head_stride
+ *        + slot*token_stride + dim                      (in elements)
+ *     The default strides are those of the [num_pages, num_layers,
+ *     num_kv_heads, page_size, head_dim] pool of kunserve/worker.py:168-176.
+ *   - Page tables are CSR: pages of sequence b are
+ *     indices[indptr[b] .. indptr[b+1]), token t of sequence b lives in page
+ *     indices[indptr[b] + t / page_size] at slot t % page_size
+ *     (kunserve/block_manager.py:786-795).
+ */
+#ifndef KUNSERVE_HIP_H
+#define KUNSERVE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* kunserve_stream_t; /* == hipStream_t */
+
+enum {
+  KUNSERVE_OK = 0,
+  KUNSERVE_EINVAL = -1,     /* bad argument (shape, stride, alignment, NULL) */
+  KUNSERVE_ERANGE = -2,     /* page / block id outside the pool              */
+  KUNSERVE_ENOSPC = -3,     /* caller buffer (plan, workspace) too small     */
+  KUNSERVE_EUNSUPPORTED = -4, /* head_dim / page_size / GQA not compiled   */
+  KUNSERVE_EHIP = -5        /* a HIP runtime call failed                     */
+};
+
+/* Paged KV pool (separate K and V pools with identical strides). */
+typedef struct {
+  void* k;                 /* device, fp16 */
+  void* v;                 /* device, fp16 */
+  int64_t num_pages;       /* page ids must lie in [0, num_pages)            */
+  int64_t page_stride;     /* elements between consecutive pages             */
+  int64_t layer_stride;
+  int64_t head_stride;
+  int64_t token_stride;    /* elements between consecutive slots of a page   */
+  int32_t num_layers;
+  int32_t num_kv_heads;
+  int32_t page_size;       /* tokens per page; power of two, >= 4            */
+  int32_t head_dim;        /* 64, 128 or 256                                 */
+} kunserve_kv_pool;
+
+/* Per-step page table in CSR form, device resident. */
+typedef struct {
+  const int32_t* indptr_dev;   /* [num_seqs + 1]                             */
+  const int32_t* indices_dev;  /* [indptr[num_seqs]] page ids                */
+  const int32_t* kv_len_dev;   /* [num_seqs] tokens in the cache after append */
+  int32_t num_seqs;
+} kunserve_page_table;
+
+/* Strided fp16 activation tensor [num_tokens, num_heads, head_dim]
+ * (head_dim contiguous). */
+typedef struct {
+  void* data;              /* device, fp16 */
+  int64_t token_stride;    /* elements */
+  int64_t head_stride;     /* elements */
+} kunserve_tensor3;
+
+/* ---------------------------------------------------------------- misc */
+
+/* Library ABI version (major*100 + minor). */
+int32_t kunserve_version(void);
+
+/* Message of the last error raised on the calling thread ("" if none). */
+const char* kunserve_last_error(void);
+
+/* ------------------------------------------------------- block copy (A8) */
+
+/* LlamaOp.local_copy_blocks (kunserve/worker.py:818-823): for each i,
+ * block dst_ids[i] := block src_ids[i] for K and V, all layers, same device.
+ * Ids are device int32 arrays of length n. A block is num_layers slabs of
+ * num_kv_heads*page_size*head_dim elements. Source and destination sets
+ * must not overlap (the kernel copies all pairs concurrently). */
+int kunserve_copy_blocks(const kunserve_kv_pool* pool,
+                         const int32_t* src_ids_dev, const int32_t* dst_ids_dev,
+                         int64_t n, kunserve_stream_t stream);
+
+/* kv_exchange phase 1 "pack" (kunserve/flash_backend.py:930-985): gather
+ * layers [layer_begin, layer_end) of pages page_ids[0..n) into a contiguous
+ * scratch buffer laid out [layer_end-layer_begin][n][2 (K,V)][num_kv_heads]
+ * [page_size][head_dim] (fp16, densely packed). */
+int kunserve_kv_pack(const kunserve_kv_pool* pool, int32_t layer_begin,
+                     int32_t layer_end, const int32_t* page_ids_dev, int64_t n,
+                     void* scratch_dev, int64_t scratch_bytes,
+                     kunserve_stream_t stream);
+
+/* kv_exchange phase 3 "scatter": inverse of kunserve_kv_pack — write the
+ * scratch layout into pages page_ids[0..n) (fused page ids on the receiver,
+ * kunserve/block_manager.py:755-763). */
+int kunserve_kv_scatter(const kunserve_kv_pool* pool, int32_t layer_begin,
+                        int32_t layer_end, const int32_t* page_ids_dev,
+                        int64_t n, const void* scratch_dev,
+                        int64_t scratch_bytes, kunserve_stream_t stream);
+
+/* Bytes of scratch that kunserve_kv_pack / kunserve_kv_scatter need. */
+int64_t kunserve_kv_pack_bytes(const kunserve_kv_pool* pool, int32_t num_layers,
+                               int64_t n);
+
+/* ------------------------------------------------------------ swap (A7) */
+
+/* torch.ops.swapping_ops.swap (kunserve/worker.py:646-650,673-681):
+ * for each i, copy whole block src_ids[i] -> dst_ids[i] for K and V.
+ * is_swap_in != 0: host (pinned) pool -> device pool; else device -> host.
+ * Ids are host arrays. Block b of a pool is the contiguous byte range
+ * [b*block_bytes, (b+1)*block_bytes). Consecutive runs of ids are merged
+ * into one DMA copy. Enqueued on `stream`; does not synchronise. */
+int kunserve_swap_blocks(const int64_t* src_ids_host,
+                         const int64_t* dst_ids_host, int64_t n,
+                         int32_t is_swap_in, void* k_cache_dev,
+                         void* v_cache_dev, int64_t num_gpu_blocks,
+                         void* k_swap_host, void* v_swap_host,
+                         int64_t num_cpu_blocks, int64_t block_bytes,
+                         kunserve_stream_t stream);
+
+/* --------------------------------------------------- K/V append (A5 i) */
+
+/* Append new tokens' K and V into the pool for one layer. Row b owns new
+ * tokens [q_indptr[b], q_indptr[b+1]) of k_new / v_new ([num_tokens,
+ * num_kv_heads, head_dim]); token i of row b goes to position
+ * kv_len[b] - q_len[b] + i, i.e. page indices[indptr[b] + pos/page_size],
+ * slot pos % page_size (kunserve/request.py:447-462). */
+int kunserve_append_kv(const kunserve_kv_pool* pool, int32_t layer,
+                       const kunserve_page_table* table,
+                       const int32_t* q_indptr_dev, int32_t num_tokens,
+                       const kunserve_tensor3* k_new,
+                       const kunserve_tensor3* v_new,
+                       kunserve_stream_t stream);
+
+/* ---------------------------------------------- decode attention (A4) */
+
+typedef struct {
+  int32_t num_work;      /* decode work items (partitions)                */
+  int32_t num_merge;     /* sequences split over more than one partition  */
+  int32_t num_slots;     /* partial-result slots used                     */
+  int32_t part_tokens;   /* partition length in tokens                    */
+  int32_t group_size;    /* q heads handled per workgroup                 */
+  int32_t plan_ints;     /* int32 entries of the plan buffer in use       */
+} kunserve_decode_plan_info;
+
+/* Upper bound of the plan buffer length (int32 entries) for these lengths. */
+int64_t kunserve_decode_plan_bound(const int32_t* kv_len_host,
+                                   int32_t num_seqs);
+
+/* Host-side plan, shared by every layer of one step (decode rows only).
+ * Splits each sequence into partitions of part_tokens (0 = choose from
+ * num_cus so that the grid fills the device), orders the work, and writes
+ * it to plan_host (int32, upload it to the device as-is). */
+int kunserve_decode_plan(const int32_t* kv_len_host, int32_t num_seqs,
+                         int32_t num_qo_heads, int32_t num_kv_heads,
+                         int32_t num_cus, int32_t part_tokens,
+                         int32_t* plan_host, int64_t plan_capacity,
+                         kunserve_decode_plan_info* info);
+
+/* Workspace bytes needed by kunserve_paged_decode for this plan. */
+int64_t kunserve_decode_workspace_bytes(const kunserve_decode_plan_info* info,
+                                        int32_t num_qo_heads,
+                                        int32_t head_dim);
+
+/* o[b, h, :] = softmax(q[b, h, :] . K[b, g(h)]^T * sm_scale) . V[b, g(h)]
+ * over the kv_len[b] tokens of sequence b in layer `layer`, with
+ * g(h) = h / (num_qo_heads / num_kv_heads). q and out are
+ * [num_seqs, num_qo_heads, head_dim] fp16; fp32 accumulation. */
+int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer,
+                          const kunserve_page_table* table,
+                          const kunserve_tensor3* q, kunserve_tensor3* out,
+                          int32_t num_qo_heads, float sm_scale,
+                          const int32_t* plan_dev,
+                          const kunserve_decode_plan_info* info,
+                          void* workspace_dev, int64_t workspace_bytes,
+                          kunserve_stream_t stream);
+
+/* ------------------------------------- chunked-prefill attention (A5 ii) */
+
+typedef struct {
+  int32_t num_tiles;     /* (row, q-tile) work items                       */
+  int32_t tile_q;        /* q rows per tile                                */
+  int32_t plan_ints;
+} kunserve_prefill_plan_info;
+
+/* Host-side plan: tiles the ragged q rows (q_len[b] = q_indptr[b+1] -
+ * q_indptr[b]) into tiles of tile_q rows. */
+int kunserve_prefill_plan(const int32_t* q_indptr_host,
+                          const int32_t* kv_len_host, int32_t num_seqs,
+                          int32_t* plan_host, int64_t plan_capacity,
+                          kunserve_prefill_plan_info* info);
+
+/* Causal attention of the q_len[b] new rows of each sequence against its
+ * kv_len[b] cached tokens (new ones already appended): q row i of
+ * sequence b sees positions [0, kv_len[b] - q_len[b] + i]. q and out are
+ * [num_tokens, num_qo_heads, head_dim] fp16 with rows grouped by q_indptr.
+ * fp16 MFMA for Q.K^T and P.V, fp32 accumulation and softmax. */
+int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
+                           const kunserve_page_table* table,
+                           const int32_t* q_indptr_dev,
+                           const kunserve_tensor3* q, kunserve_tensor3* out,
+                           int32_t num_qo_heads, float sm_scale,
+                           const int32_t* plan_dev,
+                           const kunserve_prefill_plan_info* info,
+                           kunserve_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KUNSERVE_HIP_H */

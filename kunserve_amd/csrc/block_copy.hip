@@ -1,0 +1,271 @@
+// KV block movement for the paged pool: device block copy
+// (LlamaOp.local_copy_blocks, kunserve/worker.py:818-823), kv_exchange pack
+// and scatter (kunserve/flash_backend.py:930-985) and GPU<->host swap
+// (torch.ops.swapping_ops.swap, kunserve/worker.py:646-650,673-681).
+//
+// Copy and pack/scatter are HBM-bound: every byte is read once and written
+// once. One kernel serves all three: it walks "spans" (contiguous byte
+// ranges) addressed through an optional id list on each side, and each
+// workgroup streams a 32 KiB chunk of one span with 16-byte vector loads,
+// eight loads in flight per lane before the first store.
+#include "common.hpp"
+
+namespace kunserve {
+namespace {
+
+constexpr int kCopyThreads = 256;
+constexpr int kCopyUnroll = 8;
+constexpr int64_t kCopyChunk = int64_t(kCopyThreads) * 16 * kCopyUnroll;  // 32 KiB
+
+// One side of a copy: span s of item j lives at
+//   base + id(j) * pitch + s * span_stride      (bytes)
+// with id(j) = ids ? ids[j] : j. Items whose id is outside [0, limit) are
+// skipped (the host validates ids; this only keeps a bad id from faulting).
+struct Side {
+  char* base;
+  const int32_t* ids;
+  int64_t pitch;
+  int64_t span_stride;
+  int64_t limit;
+};
+
+struct CopyJob {
+  Side src;
+  Side dst;
+  int64_t n;             // items
+  int32_t spans;         // spans per item
+  int64_t span_bytes;    // multiple of 16
+  int64_t chunks;        // ceil(span_bytes / kCopyChunk)
+};
+
+// Grid: x = item, y = chunk of the span, z = span. All index math is
+// scalar; each lane keeps 8 x 16 bytes in flight.
+__global__ __launch_bounds__(kCopyThreads) void span_copy_kernel(CopyJob job) {
+  const int64_t item = blockIdx.x;
+  const int64_t chunk = blockIdx.y;
+  const int64_t span = blockIdx.z;
+
+  const int64_t sid = job.src.ids ? job.src.ids[item] : item;
+  const int64_t did = job.dst.ids ? job.dst.ids[item] : item;
+  if (sid < 0 || sid >= job.src.limit || did < 0 || did >= job.dst.limit) return;
+
+  const int64_t start = chunk * kCopyChunk;
+  const char* src = job.src.base + sid * job.src.pitch + span * job.src.span_stride + start;
+  char* dst = job.dst.base + did * job.dst.pitch + span * job.dst.span_stride + start;
+  const int32_t avail = int32_t(min<int64_t>(job.span_bytes - start, kCopyChunk));
+  const int32_t lane_off = int32_t(threadIdx.x) * 16;
+
+  u32x4 buf[kCopyUnroll];
+  if (avail == kCopyChunk) {
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u)
+      buf[u] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(src + lane_off + u * kCopyThreads * 16));
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u)
+      __builtin_nontemporal_store(buf[u],
+                                  reinterpret_cast<u32x4*>(dst + lane_off + u * kCopyThreads * 16));
+  } else {
+    // Last, partial chunk of a span.
+    for (int32_t off = lane_off; off < avail; off += kCopyThreads * 16)
+      *reinterpret_cast<u32x4*>(dst + off) = *reinterpret_cast<const u32x4*>(src + off);
+  }
+}
+
+int launch_job(const CopyJob& job, hipStream_t stream) {
+  if (job.n == 0 || job.spans == 0) return KUNSERVE_OK;
+  KSV_CHECK_ARG(job.n < (int64_t(1) << 31), "copy of %lld items exceeds one launch",
+                (long long)job.n);
+  KSV_CHECK_ARG(job.chunks <= 65535 && job.spans <= 65535,
+                "span of %lld bytes x %d spans exceeds the launch geometry",
+                (long long)job.span_bytes, job.spans);
+  dim3 grid(static_cast<unsigned>(job.n), static_cast<unsigned>(job.chunks),
+            static_cast<unsigned>(job.spans));
+  span_copy_kernel<<<grid, kCopyThreads, 0, stream>>>(job);
+  KSV_CHECK_LAUNCH();
+  return KUNSERVE_OK;
+}
+
+int launch_jobs(const CopyJob& a, const CopyJob* b, hipStream_t stream) {
+  int rc = launch_job(a, stream);
+  if (rc || !b) return rc;
+  return launch_job(*b, stream);
+}
+
+// Byte geometry of one page of one layer ("slab") in the pool.
+struct SlabGeom {
+  int64_t slab_bytes;     // num_kv_heads * page_size * head_dim * 2
+  bool slab_dense;        // slab is one contiguous range
+  bool block_dense;       // all layers of a page are one contiguous range
+};
+
+SlabGeom slab_geom(const kunserve_kv_pool* p) {
+  SlabGeom g;
+  const int64_t tok = p->head_dim;
+  const int64_t head = int64_t(p->page_size) * tok;
+  const int64_t slab = int64_t(p->num_kv_heads) * head;
+  g.slab_bytes = slab * 2;
+  g.slab_dense = p->token_stride == tok && (p->num_kv_heads == 1 || p->head_stride == head);
+  g.block_dense = g.slab_dense && (p->num_layers == 1 || p->layer_stride == slab);
+  return g;
+}
+
+}  // namespace
+}  // namespace kunserve
+
+using namespace kunserve;
+
+extern "C" int kunserve_copy_blocks(const kunserve_kv_pool* pool, const int32_t* src_ids_dev,
+                                    const int32_t* dst_ids_dev, int64_t n,
+                                    kunserve_stream_t stream) {
+  clear_error();
+  int rc = check_pool(pool, false);
+  if (rc) return rc;
+  KSV_CHECK_ARG(n >= 0, "n < 0");
+  if (n == 0) return KUNSERVE_OK;
+  KSV_CHECK_ARG(src_ids_dev && dst_ids_dev, "null id array");
+  const SlabGeom g = slab_geom(pool);
+  KSV_CHECK_ARG(g.slab_dense, "copy_blocks needs dense [heads, page_size, head_dim] slabs");
+  CopyJob job{};
+  job.n = n;
+  if (g.block_dense) {
+    job.spans = 1;
+    job.span_bytes = g.slab_bytes * pool->num_layers;
+  } else {
+    job.spans = pool->num_layers;
+    job.span_bytes = g.slab_bytes;
+  }
+  job.chunks = (job.span_bytes + kCopyChunk - 1) / kCopyChunk;
+  for (Side* s : {&job.src, &job.dst}) {
+    s->pitch = pool->page_stride * 2;
+    s->span_stride = pool->layer_stride * 2;
+    s->limit = pool->num_pages;
+  }
+  job.src.ids = src_ids_dev;
+  job.dst.ids = dst_ids_dev;
+  CopyJob jv = job;
+  job.src.base = job.dst.base = static_cast<char*>(pool->k);
+  jv.src.base = jv.dst.base = static_cast<char*>(pool->v);
+  return launch_jobs(job, &jv, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t kunserve_kv_pack_bytes(const kunserve_kv_pool* pool, int32_t num_layers,
+                                          int64_t n) {
+  if (!pool || num_layers < 0 || n < 0) return -1;
+  return int64_t(num_layers) * n * 2 * slab_geom(pool).slab_bytes;
+}
+
+namespace {
+// Pack (to_scratch) or scatter: pool pages <-> scratch
+// [layers][n][K|V][num_kv_heads][page_size][head_dim].
+int pack_or_scatter(const kunserve_kv_pool* pool, int32_t layer_begin, int32_t layer_end,
+                    const int32_t* page_ids_dev, int64_t n, char* scratch,
+                    int64_t scratch_bytes, bool to_scratch, hipStream_t stream) {
+  clear_error();
+  int rc = check_pool(pool, false);
+  if (rc) return rc;
+  KSV_CHECK_ARG(0 <= layer_begin && layer_begin <= layer_end && layer_end <= pool->num_layers,
+                "layer range [%d, %d) outside [0, %d)", layer_begin, layer_end,
+                pool->num_layers);
+  KSV_CHECK_ARG(n >= 0, "n < 0");
+  const int32_t nl = layer_end - layer_begin;
+  if (n == 0 || nl == 0) return KUNSERVE_OK;
+  KSV_CHECK_ARG(page_ids_dev && scratch, "null pointer");
+  const SlabGeom g = slab_geom(pool);
+  KSV_CHECK_ARG(g.slab_dense, "pack/scatter needs dense [heads, page_size, head_dim] slabs");
+  const int64_t need = kunserve_kv_pack_bytes(pool, nl, n);
+  if (scratch_bytes < need) {
+    set_error("scratch holds %lld bytes, %lld needed", (long long)scratch_bytes,
+              (long long)need);
+    return KUNSERVE_ENOSPC;
+  }
+  CopyJob jobs[2];
+  for (int kv = 0; kv < 2; ++kv) {
+    CopyJob& job = jobs[kv];
+    job = CopyJob{};
+    job.n = n;
+    job.spans = nl;
+    job.span_bytes = g.slab_bytes;
+    job.chunks = (job.span_bytes + kCopyChunk - 1) / kCopyChunk;
+    Side pool_side{};
+    pool_side.base = static_cast<char*>(kv ? pool->v : pool->k) +
+                     int64_t(layer_begin) * pool->layer_stride * 2;
+    pool_side.ids = page_ids_dev;
+    pool_side.pitch = pool->page_stride * 2;
+    pool_side.span_stride = pool->layer_stride * 2;
+    pool_side.limit = pool->num_pages;
+    Side scr{};
+    scr.base = scratch + kv * g.slab_bytes;
+    scr.ids = nullptr;
+    scr.pitch = 2 * g.slab_bytes;
+    scr.span_stride = n * 2 * g.slab_bytes;
+    scr.limit = n;
+    job.src = to_scratch ? pool_side : scr;
+    job.dst = to_scratch ? scr : pool_side;
+  }
+  return launch_jobs(jobs[0], &jobs[1], stream);
+}
+}  // namespace
+
+extern "C" int kunserve_kv_pack(const kunserve_kv_pool* pool, int32_t layer_begin,
+                                int32_t layer_end, const int32_t* page_ids_dev, int64_t n,
+                                void* scratch_dev, int64_t scratch_bytes,
+                                kunserve_stream_t stream) {
+  return pack_or_scatter(pool, layer_begin, layer_end, page_ids_dev, n,
+                         static_cast<char*>(scratch_dev), scratch_bytes, true,
+                         reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int kunserve_kv_scatter(const kunserve_kv_pool* pool, int32_t layer_begin,
+                                   int32_t layer_end, const int32_t* page_ids_dev, int64_t n,
+                                   const void* scratch_dev, int64_t scratch_bytes,
+                                   kunserve_stream_t stream) {
+  return pack_or_scatter(pool, layer_begin, layer_end, page_ids_dev, n,
+                         const_cast<char*>(static_cast<const char*>(scratch_dev)),
+                         scratch_bytes, false, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int kunserve_swap_blocks(const int64_t* src_ids_host, const int64_t* dst_ids_host,
+                                    int64_t n, int32_t is_swap_in, void* k_cache_dev,
+                                    void* v_cache_dev, int64_t num_gpu_blocks,
+                                    void* k_swap_host, void* v_swap_host,
+                                    int64_t num_cpu_blocks, int64_t block_bytes,
+                                    kunserve_stream_t stream) {
+  clear_error();
+  KSV_CHECK_ARG(n >= 0 && block_bytes > 0, "bad n or block_bytes");
+  if (n == 0) return KUNSERVE_OK;
+  KSV_CHECK_ARG(src_ids_host && dst_ids_host, "null id array");
+  KSV_CHECK_ARG(k_cache_dev && v_cache_dev && k_swap_host && v_swap_host, "null pool pointer");
+  const int64_t src_limit = is_swap_in ? num_cpu_blocks : num_gpu_blocks;
+  const int64_t dst_limit = is_swap_in ? num_gpu_blocks : num_cpu_blocks;
+  for (int64_t i = 0; i < n; ++i) {
+    if (src_ids_host[i] < 0 || src_ids_host[i] >= src_limit || dst_ids_host[i] < 0 ||
+        dst_ids_host[i] >= dst_limit) {
+      set_error("swap pair %lld: %lld -> %lld outside [0, %lld) -> [0, %lld)", (long long)i,
+                (long long)src_ids_host[i], (long long)dst_ids_host[i], (long long)src_limit,
+                (long long)dst_limit);
+      return KUNSERVE_ERANGE;
+    }
+  }
+  char* srcs[2] = {static_cast<char*>(is_swap_in ? k_swap_host : k_cache_dev),
+                   static_cast<char*>(is_swap_in ? v_swap_host : v_cache_dev)};
+  char* dsts[2] = {static_cast<char*>(is_swap_in ? k_cache_dev : k_swap_host),
+                   static_cast<char*>(is_swap_in ? v_cache_dev : v_swap_host)};
+  const hipMemcpyKind kind = is_swap_in ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Merge runs where both source and destination ids are consecutive.
+  int64_t i = 0;
+  while (i < n) {
+    int64_t j = i + 1;
+    while (j < n && src_ids_host[j] == src_ids_host[j - 1] + 1 &&
+           dst_ids_host[j] == dst_ids_host[j - 1] + 1)
+      ++j;
+    const int64_t bytes = (j - i) * block_bytes;
+    for (int kv = 0; kv < 2; ++kv) {
+      KSV_CHECK_HIP(hipMemcpyAsync(dsts[kv] + dst_ids_host[i] * block_bytes,
+                                   srcs[kv] + src_ids_host[i] * block_bytes, bytes, kind, s));
+    }
+    i = j;
+  }
+  return KUNSERVE_OK;
+}

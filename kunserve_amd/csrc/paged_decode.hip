@@ -1,0 +1,449 @@
+// Paged decode attention (q_len == 1 rows of LlamaOp.pforward,
+// kunserve/worker.py:298-312; head counts kunserve/models.py:55-56, page
+// size kunserve/models.py:57).
+//
+// HBM-bound: every K/V byte of a sequence is read exactly once per layer.
+// Design for gfx950 (wave64, 256 CUs):
+//  * The host plan cuts every sequence into partitions of part_tokens and
+//    orders them longest first; the grid is (work items, head groups), so
+//    mixed context lengths still give an even, device-filling grid.
+//  * A workgroup (4 waves) owns one partition of one KV head and all
+//    `G` query heads that share it (GQA: one KV read serves G heads).
+//  * The partition's slice of the page table is staged in LDS once; after
+//    that each K/V access is one 16-byte load per lane. A wave reads 1 KiB
+//    of K and 1 KiB of V per load instruction (4 tokens x 256 B for
+//    head_dim 128), four of each in flight per 16-token chunk.
+//  * Q.K uses v_dot2_f32_f16 and a DPP butterfly inside each 16-lane row;
+//    the softmax is an online (running max) softmax in fp32 kept per row,
+//    merged across rows with shuffles and across waves through LDS.
+//  * Sequences longer than one partition write fp32 partial results with
+//    their log-sum-exp (base 2); a small merge kernel combines them.
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "common.hpp"
+
+namespace kunserve {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kLoadsPerChunk = 4;        // 16-byte loads per lane per chunk (K and V each)
+constexpr int kMaxPartTokens = 4096;
+constexpr int kMinPageSize = 4;
+constexpr int kMaxPartPages = kMaxPartTokens / kMinPageSize + 2;
+constexpr int kMinPartTokens = 256;
+constexpr float kNegBig = -1.0e30f;      // finite "minus infinity" for running maxima
+
+struct DecodeArgs {
+  const f16* q;
+  int64_t q_tok, q_head;
+  f16* out;
+  int64_t o_tok, o_head;
+  const f16* k;             // pool K at the layer
+  const f16* v;
+  int64_t page_stride, head_stride, token_stride;
+  int32_t num_pages;
+  int32_t page_shift;
+  const int32_t* indptr;
+  const int32_t* indices;
+  const int32_t* work;      // [num_work][4]: seq, tok_begin, tok_end, slot (-1: direct)
+  float* part_o;            // [slots][num_qo_heads][D]
+  float* part_lse;          // [slots][num_qo_heads]
+  int32_t num_qo_heads;
+  int32_t ratio;            // num_qo_heads / num_kv_heads
+  float scale_log2;         // sm_scale * log2(e)
+};
+
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
+  constexpr int LPT = D / 8;            // lanes per token row (16 for D = 128)
+  constexpr int TPL = kWave / LPT;      // tokens per load instruction (4)
+  constexpr int CHUNK = TPL * kLoadsPerChunk;  // tokens per wave iteration (16)
+
+  __shared__ int s_pages[kMaxPartPages];
+  __shared__ float s_m[kWaves][G];
+  __shared__ float s_l[kWaves][G];
+  __shared__ float s_acc[kWaves][G][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int row = lane / LPT;
+  const int col = lane % LPT;
+
+  const int32_t* w = a.work + 4 * blockIdx.x;
+  const int seq = w[0], tb = w[1], te = w[2], slot = w[3];
+  const int hq0 = blockIdx.y * G;
+  const int hkv = hq0 / a.ratio;
+  const int page_mask = (1 << a.page_shift) - 1;
+
+  // Stage this partition's page ids; invalid ids become -1 (masked).
+  const int pb = tb >> a.page_shift;
+  const int np = te > tb ? ((te - 1) >> a.page_shift) + 1 - pb : 0;
+  const int32_t* seq_pages = a.indices + a.indptr[seq];
+  for (int i = tid; i < np; i += kThreads) {
+    const int p = seq_pages[pb + i];
+    s_pages[i] = (p >= 0 && p < a.num_pages) ? p : -1;
+  }
+
+  f16x8 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    qv[g] = load_f16x8(a.q + int64_t(seq) * a.q_tok + int64_t(hq0 + g) * a.q_head + col * 8);
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
+  }
+  __syncthreads();
+
+  const f16* kb = a.k + int64_t(hkv) * a.head_stride + col * 8;
+  const f16* vb = a.v + int64_t(hkv) * a.head_stride + col * 8;
+  const int nchunks = (te - tb + CHUNK - 1) / CHUNK;
+
+  for (int c = wave; c < nchunks; c += kWaves) {
+    const int t0 = tb + c * CHUNK;
+    f16x8 kr[kLoadsPerChunk], vr[kLoadsPerChunk];
+    bool ok[kLoadsPerChunk];
+#pragma unroll
+    for (int i = 0; i < kLoadsPerChunk; ++i) {
+      const int t = t0 + i * TPL + row;
+      const int p = t < te ? s_pages[(t >> a.page_shift) - pb] : -1;
+      ok[i] = p >= 0;
+      const int64_t off = int64_t(p) * a.page_stride + int64_t(t & page_mask) * a.token_stride;
+      if (ok[i]) {
+        kr[i] = load_f16x8(kb + off);
+        vr[i] = load_f16x8(vb + off);
+      } else {
+        kr[i] = f16x8{};
+        vr[i] = f16x8{};
+      }
+    }
+    float vf[kLoadsPerChunk][8];
+#pragma unroll
+    for (int i = 0; i < kLoadsPerChunk; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vf[i][j] = float(vr[i][j]);
+
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float s[kLoadsPerChunk];
+      float mx = m[g];
+#pragma unroll
+      for (int i = 0; i < kLoadsPerChunk; ++i) {
+        s[i] = group_sum<LPT>(dot8(qv[g], kr[i], 0.f)) * a.scale_log2;
+        s[i] = ok[i] ? s[i] : -INFINITY;
+        mx = fmaxf(mx, s[i]);
+      }
+      const float alpha = fast_exp2(m[g] - mx);
+      m[g] = mx;
+      float p[kLoadsPerChunk];
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < kLoadsPerChunk; ++i) {
+        p[i] = fast_exp2(s[i] - mx);
+        ps += p[i];
+      }
+      l[g] = l[g] * alpha + ps;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float x = acc[g][j] * alpha;
+#pragma unroll
+        for (int i = 0; i < kLoadsPerChunk; ++i) x = fmaf(p[i], vf[i][j], x);
+        acc[g][j] = x;
+      }
+    }
+  }
+
+  // Merge the TPL rows of each wave (lanes col, col+LPT, ...).
+#pragma unroll
+  for (int off = LPT; off < kWave; off <<= 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float m2 = __shfl_xor(m[g], off);
+      const float l2 = __shfl_xor(l[g], off);
+      const float mx = fmaxf(m[g], m2);
+      const float f1 = fast_exp2(m[g] - mx), f2 = fast_exp2(m2 - mx);
+      m[g] = mx;
+      l[g] = l[g] * f1 + l2 * f2;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a2 = __shfl_xor(acc[g][j], off);
+        acc[g][j] = acc[g][j] * f1 + a2 * f2;
+      }
+    }
+  }
+  if (row == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (col == 0) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s_acc[wave][g][col * 8 + j] = acc[g][j];
+    }
+  }
+  __syncthreads();
+
+  // Merge the waves and write the output (direct) or a partial (split).
+  for (int idx = tid; idx < G * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    float mx = kNegBig;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) mx = fmaxf(mx, s_m[wv][g]);
+    float lsum = 0.f, o = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) {
+      const float f = fast_exp2(s_m[wv][g] - mx);
+      lsum += s_l[wv][g] * f;
+      o += s_acc[wv][g][d] * f;
+    }
+    const float r = lsum > 0.f ? o / lsum : 0.f;
+    const int hq = hq0 + g;
+    if (slot < 0) {
+      a.out[int64_t(seq) * a.o_tok + int64_t(hq) * a.o_head + d] = f16(r);
+    } else {
+      a.part_o[(int64_t(slot) * a.num_qo_heads + hq) * D + d] = r;
+      if (d == 0)
+        a.part_lse[int64_t(slot) * a.num_qo_heads + hq] =
+            lsum > 0.f ? mx + __log2f(lsum) : -INFINITY;
+    }
+  }
+}
+
+// Combines the partitions of split sequences: one workgroup per
+// (sequence, q head), one thread per dimension.
+template <int D>
+__global__ __launch_bounds__(D) void decode_merge_kernel(const int32_t* merges,
+                                                         const float* part_o,
+                                                         const float* part_lse, f16* out,
+                                                         int64_t o_tok, int64_t o_head,
+                                                         int32_t num_qo_heads) {
+  const int32_t* mg = merges + 4 * blockIdx.x;
+  const int seq = mg[0], s0 = mg[1], n = mg[2];
+  const int hq = blockIdx.y;
+  const int d = threadIdx.x;
+  float mx = -INFINITY;
+  for (int j = 0; j < n; ++j) mx = fmaxf(mx, part_lse[int64_t(s0 + j) * num_qo_heads + hq]);
+  float wsum = 0.f, o = 0.f;
+  if (mx > -INFINITY) {
+    for (int j = 0; j < n; ++j) {
+      const int64_t sj = int64_t(s0 + j) * num_qo_heads + hq;
+      const float f = fast_exp2(part_lse[sj] - mx);
+      wsum += f;
+      o += f * part_o[sj * D + d];
+    }
+  }
+  out[int64_t(seq) * o_tok + int64_t(hq) * o_head + d] = f16(wsum > 0.f ? o / wsum : 0.f);
+}
+
+int pick_group(int ratio) {
+  for (int g : {8, 4, 2}) {
+    if (ratio % g == 0) return g;
+  }
+  return 1;
+}
+
+template <int D>
+int launch_decode(const DecodeArgs& a, int group, dim3 grid, hipStream_t s) {
+  switch (group) {
+    case 1: paged_decode_kernel<D, 1><<<grid, kThreads, 0, s>>>(a); break;
+    case 2: paged_decode_kernel<D, 2><<<grid, kThreads, 0, s>>>(a); break;
+    case 4: paged_decode_kernel<D, 4><<<grid, kThreads, 0, s>>>(a); break;
+    case 8: paged_decode_kernel<D, 8><<<grid, kThreads, 0, s>>>(a); break;
+    default: set_error("unsupported group size %d", group); return KUNSERVE_EUNSUPPORTED;
+  }
+  KSV_CHECK_LAUNCH();
+  return KUNSERVE_OK;
+}
+
+template <int D>
+int launch_merge(const int32_t* merges, int num_merge, const float* po, const float* pl, f16* out,
+                 int64_t o_tok, int64_t o_head, int hq, hipStream_t s) {
+  dim3 grid(num_merge, hq);
+  decode_merge_kernel<D><<<grid, D, 0, s>>>(merges, po, pl, out, o_tok, o_head, hq);
+  KSV_CHECK_LAUNCH();
+  return KUNSERVE_OK;
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+}  // namespace kunserve
+
+using namespace kunserve;
+
+extern "C" int64_t kunserve_decode_plan_bound(const int32_t* kv_len_host, int32_t num_seqs) {
+  if (num_seqs < 0 || (num_seqs > 0 && !kv_len_host)) return -1;
+  int64_t parts = 0;
+  for (int32_t b = 0; b < num_seqs; ++b)
+    parts += std::max<int64_t>(1, ceil_div(std::max(kv_len_host[b], 0), kMinPartTokens));
+  return 4 * (parts + num_seqs);
+}
+
+extern "C" int kunserve_decode_plan(const int32_t* kv_len_host, int32_t num_seqs,
+                                    int32_t num_qo_heads, int32_t num_kv_heads, int32_t num_cus,
+                                    int32_t part_tokens, int32_t* plan_host,
+                                    int64_t plan_capacity, kunserve_decode_plan_info* info) {
+  clear_error();
+  KSV_CHECK_ARG(info && plan_host, "null plan buffer or info");
+  KSV_CHECK_ARG(num_seqs >= 0 && (num_seqs == 0 || kv_len_host), "bad kv_len / num_seqs");
+  KSV_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && num_qo_heads % num_kv_heads == 0,
+                "num_qo_heads %d not a multiple of num_kv_heads %d", num_qo_heads, num_kv_heads);
+  for (int32_t b = 0; b < num_seqs; ++b)
+    KSV_CHECK_ARG(kv_len_host[b] >= 0, "kv_len[%d] = %d < 0", b, kv_len_host[b]);
+  const int group = pick_group(num_qo_heads / num_kv_heads);
+  const int64_t head_groups = num_qo_heads / group;
+
+  if (part_tokens == 0) {
+    // Largest partition that still gives >= 8 workgroups per CU; short
+    // batches fall back to the minimum partition.
+    const int64_t target = int64_t(std::max(num_cus, 1)) * 8;
+    part_tokens = kMinPartTokens;
+    for (int cand = kMaxPartTokens; cand >= kMinPartTokens; cand >>= 1) {
+      int64_t wgs = 0;
+      for (int32_t b = 0; b < num_seqs; ++b)
+        wgs += std::max<int64_t>(1, ceil_div(kv_len_host[b], cand));
+      if (wgs * head_groups >= target) {
+        part_tokens = cand;
+        break;
+      }
+    }
+  }
+  KSV_CHECK_ARG(part_tokens >= kMinPartTokens && part_tokens <= kMaxPartTokens &&
+                    part_tokens % 64 == 0,
+                "part_tokens %d must be a multiple of 64 in [%d, %d]", part_tokens,
+                kMinPartTokens, kMaxPartTokens);
+
+  // Work items: (seq, begin, end, slot). Full partitions first, then tails
+  // by decreasing length, so the longest items start first.
+  struct Item { int32_t seq, b, e, slot; };
+  std::vector<Item> items;
+  std::vector<int32_t> merges;
+  int32_t slots = 0;
+  for (int32_t b = 0; b < num_seqs; ++b) {
+    const int32_t len = kv_len_host[b];
+    const int32_t n = std::max<int32_t>(1, int32_t(ceil_div(len, part_tokens)));
+    if (n == 1) {
+      items.push_back({b, 0, len, -1});
+    } else {
+      merges.insert(merges.end(), {b, slots, n, 0});
+      for (int32_t j = 0; j < n; ++j)
+        items.push_back({b, j * part_tokens, std::min(len, (j + 1) * part_tokens), slots + j});
+      slots += n;
+    }
+  }
+  std::stable_sort(items.begin(), items.end(),
+                   [](const Item& x, const Item& y) { return (x.e - x.b) > (y.e - y.b); });
+  const int64_t need = 4 * int64_t(items.size()) + int64_t(merges.size());
+  if (need > plan_capacity) {
+    set_error("plan needs %lld ints, capacity %lld", (long long)need, (long long)plan_capacity);
+    return KUNSERVE_ENOSPC;
+  }
+  int32_t* p = plan_host;
+  for (const Item& it : items) {
+    *p++ = it.seq;
+    *p++ = it.b;
+    *p++ = it.e;
+    *p++ = it.slot;
+  }
+  std::copy(merges.begin(), merges.end(), p);
+  info->num_work = int32_t(items.size());
+  info->num_merge = int32_t(merges.size() / 4);
+  info->num_slots = slots;
+  info->part_tokens = part_tokens;
+  info->group_size = group;
+  info->plan_ints = int32_t(need);
+  return KUNSERVE_OK;
+}
+
+extern "C" int64_t kunserve_decode_workspace_bytes(const kunserve_decode_plan_info* info,
+                                                   int32_t num_qo_heads, int32_t head_dim) {
+  if (!info || num_qo_heads <= 0 || head_dim <= 0) return -1;
+  const int64_t slots = info->num_slots;
+  return slots * num_qo_heads * (int64_t(head_dim) + 1) * int64_t(sizeof(float));
+}
+
+extern "C" int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer,
+                                     const kunserve_page_table* table,
+                                     const kunserve_tensor3* q, kunserve_tensor3* out,
+                                     int32_t num_qo_heads, float sm_scale,
+                                     const int32_t* plan_dev,
+                                     const kunserve_decode_plan_info* info, void* workspace_dev,
+                                     int64_t workspace_bytes, kunserve_stream_t stream) {
+  clear_error();
+  int rc = check_pool(pool, true);
+  if (rc) return rc;
+  KSV_CHECK_ARG(table && q && out && info, "null argument");
+  KSV_CHECK_ARG(layer >= 0 && layer < pool->num_layers, "layer %d outside [0, %d)", layer,
+                pool->num_layers);
+  KSV_CHECK_ARG(num_qo_heads > 0 && num_qo_heads % pool->num_kv_heads == 0,
+                "num_qo_heads %d not a multiple of num_kv_heads %d", num_qo_heads,
+                pool->num_kv_heads);
+  const int ratio = num_qo_heads / pool->num_kv_heads;
+  KSV_CHECK_ARG(info->group_size >= 1 && ratio % info->group_size == 0,
+                "plan group size %d does not divide the GQA ratio %d", info->group_size, ratio);
+  if (info->num_work == 0) return KUNSERVE_OK;
+  KSV_CHECK_ARG(plan_dev && table->indptr_dev && table->indices_dev, "null plan or table");
+  KSV_CHECK_ARG(q->data && out->data && aligned16(q->data) &&
+                    (q->token_stride % 8) == 0 && (q->head_stride % 8) == 0,
+                "q must be 16-byte aligned with strides that are multiples of 8");
+  const int64_t ws_need = kunserve_decode_workspace_bytes(info, num_qo_heads, pool->head_dim);
+  if (info->num_slots > 0 && (workspace_bytes < ws_need || !workspace_dev)) {
+    set_error("decode workspace holds %lld bytes, %lld needed", (long long)workspace_bytes,
+              (long long)ws_need);
+    return KUNSERVE_ENOSPC;
+  }
+  DecodeArgs a{};
+  a.q = static_cast<const f16*>(q->data);
+  a.q_tok = q->token_stride;
+  a.q_head = q->head_stride;
+  a.out = static_cast<f16*>(out->data);
+  a.o_tok = out->token_stride;
+  a.o_head = out->head_stride;
+  a.k = static_cast<const f16*>(pool->k) + int64_t(layer) * pool->layer_stride;
+  a.v = static_cast<const f16*>(pool->v) + int64_t(layer) * pool->layer_stride;
+  a.page_stride = pool->page_stride;
+  a.head_stride = pool->head_stride;
+  a.token_stride = pool->token_stride;
+  a.num_pages = int32_t(pool->num_pages);
+  a.page_shift = __builtin_ctz(pool->page_size);
+  a.indptr = table->indptr_dev;
+  a.indices = table->indices_dev;
+  a.work = plan_dev;
+  float* ws = static_cast<float*>(workspace_dev);
+  a.part_o = ws;
+  a.part_lse = ws ? ws + int64_t(info->num_slots) * num_qo_heads * pool->head_dim : nullptr;
+  a.num_qo_heads = num_qo_heads;
+  a.ratio = ratio;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid(info->num_work, num_qo_heads / info->group_size);
+  switch (pool->head_dim) {
+    case 64: rc = launch_decode<64>(a, info->group_size, grid, s); break;
+    case 128: rc = launch_decode<128>(a, info->group_size, grid, s); break;
+    case 256: rc = launch_decode<256>(a, info->group_size, grid, s); break;
+    default: set_error("head_dim %d not compiled", pool->head_dim); return KUNSERVE_EUNSUPPORTED;
+  }
+  if (rc || info->num_merge == 0) return rc;
+  const int32_t* merges = plan_dev + 4 * int64_t(info->num_work);
+  switch (pool->head_dim) {
+    case 64:
+      return launch_merge<64>(merges, info->num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
+                              a.o_head, num_qo_heads, s);
+    case 128:
+      return launch_merge<128>(merges, info->num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
+                               a.o_head, num_qo_heads, s);
+    default:
+      return launch_merge<256>(merges, info->num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
+                               a.o_head, num_qo_heads, s);
+  }
+}

@@ -1,0 +1,121 @@
+"""LlamaOp: the KV-cache side of torch.classes.gpt_ops.LlamaOp.
+
+The reference constructs LlamaOp with twelve ints (kunserve/models.py:52-65)
+and calls, on the paged-KV path:
+  * pforward(...)            kunserve/worker.py:298-312  (attention stage here)
+  * local_copy_blocks(...)   kunserve/worker.py:818-823
+  * kv_exchange(...)         kunserve/worker.py:514-532  (pack / scatter here)
+
+This class keeps those names, argument orders and meanings. It owns the KV
+pool, sized from max_num_pages at construction, exactly as the reference's
+LlamaOp owns kv_data (kunserve/models.py:53). The dense parts of pforward
+(QKV / O / MLP GEMMs, RoPE, sampling) are outside this library: pforward
+here takes the step's host arguments and returns an AttentionStep whose
+run(layer, q, k, v) is the per-layer attention stage.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from .paged_kv import AttentionStep, KVPool, copy_blocks, kv_pack, kv_scatter
+
+
+class LlamaOp:
+    def __init__(self, max_num_pages: int, layers: int, qo_head: int, kv_head: int,
+                 page_size: int, head_size: int, inter_size: int, vocab_size: int,
+                 max_batch_size: int, max_batch_tokens: int, max_position_embeddings: int,
+                 tensor_parallel_size: int, device: Optional[torch.device] = None):
+        if qo_head % kv_head:
+            raise ValueError(f"qo_head {qo_head} is not a multiple of kv_head {kv_head}")
+        self.max_num_pages = max_num_pages
+        self.layers = layers
+        self.qo_head = qo_head
+        self.kv_head = kv_head
+        self.page_size = page_size
+        self.head_size = head_size
+        self.inter_size = inter_size
+        self.vocab_size = vocab_size
+        self.max_batch_size = max_batch_size
+        self.max_batch_tokens = max_batch_tokens
+        self.max_position_embeddings = max_position_embeddings
+        self.tensor_parallel_size = tensor_parallel_size
+        dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.pool = KVPool.allocate(max_num_pages, layers, kv_head, page_size, head_size, dev)
+
+    # -------------------------------------------------------------- pforward
+
+    def pforward(self, num_requests: int, num_tokens: int, max_num_pages: int,
+                 local_layer_start: int, local_layer_end: int,
+                 input_tokens_batched: List[List[int]], first_token_indexes: List[int],
+                 is_prefill_requests: List[int], pages_of_reqs: List[List[int]],
+                 num_restore_requests: int = 0, pages_of_pp: Optional[List[List[int]]] = None,
+                 pages_of_dp: Optional[List[List[int]]] = None, receiver_rank: int = 0
+                 ) -> AttentionStep:
+        """Prepares the attention stage of one step (kunserve/worker.py:270-312).
+
+        Argument meanings follow kunserve/flash_backend.py:2448-2469. The
+        live-restore arguments (num_restore_requests, pages_of_pp,
+        pages_of_dp, receiver_rank) are accepted for signature parity; the
+        reference caller passes num_restore_requests = 0
+        (kunserve/flash_backend.py:2465).
+        """
+        if len(input_tokens_batched) != num_requests or len(pages_of_reqs) != num_requests:
+            raise ValueError("num_requests does not match the per-row argument lists")
+        q_lens = [len(t) for t in input_tokens_batched]
+        if sum(q_lens) != num_tokens:
+            raise ValueError(f"num_tokens {num_tokens} != {sum(q_lens)} input tokens")
+        if not 0 <= local_layer_start <= local_layer_end <= self.layers:
+            raise ValueError("local layer range outside the model")
+        if max_num_pages > self.max_num_pages:
+            raise ValueError(f"max_num_pages {max_num_pages} exceeds the pool "
+                             f"({self.max_num_pages})")
+        if num_restore_requests:
+            raise NotImplementedError("live KV restore inside pforward is not part of this path")
+        step = AttentionStep(self.pool, self.qo_head, q_lens, first_token_indexes,
+                             is_prefill_requests, pages_of_reqs)
+        step.layer_range = (local_layer_start, local_layer_end)
+        return step
+
+    # ------------------------------------------------------ block movement
+
+    def local_copy_blocks(self, max_num_pages: int, all_ex_blocks: Sequence[int],
+                          all_base_blocks: Sequence[int]) -> None:
+        """Copies extend-region blocks into base-region blocks, all layers
+        (kunserve/worker.py:818-823; caller kunserve/flash_backend.py:1116-1123)."""
+        if len(all_ex_blocks) != len(all_base_blocks):
+            raise ValueError("ex and base block lists differ in length")
+        ids = np.asarray(list(all_ex_blocks) + list(all_base_blocks), dtype=np.int64)
+        if ids.size and (ids.min() < 0 or ids.max() >= min(max_num_pages, self.max_num_pages)):
+            raise IndexError(f"block id outside [0, {min(max_num_pages, self.max_num_pages)})")
+        if len(set(all_ex_blocks) & set(all_base_blocks)):
+            raise ValueError("source and destination blocks overlap")
+        copy_blocks(self.pool, all_ex_blocks, all_base_blocks)
+
+    def kv_exchange_pack(self, page_ids: Sequence[int], layer_begin: int, layer_end: int,
+                         scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """kv_exchange phase 1: gathers the sender's pages (sorted pre-fusion
+        local ids, kunserve/flash_backend.py:913-928) for layers
+        [layer_begin, layer_end) into one contiguous buffer."""
+        return kv_pack(self.pool, layer_begin, layer_end, page_ids, scratch)
+
+    def kv_exchange_scatter(self, page_ids: Sequence[int], layer_begin: int, layer_end: int,
+                            scratch: torch.Tensor) -> None:
+        """kv_exchange phase 3: writes received pages into fused page ids
+        (kunserve/block_manager.py:755-763)."""
+        kv_scatter(self.pool, layer_begin, layer_end, page_ids, scratch)
+
+    def kv_exchange(self, pages_of_instances: List[List[int]], pp_rank: int, pp_size: int,
+                    group_rank: int, group_size: int, num_base_blocks: int,
+                    num_extend_blocks: int) -> None:
+        """kunserve/worker.py:514-532. With group_size == 1 nothing moves.
+        A multi-instance exchange needs the RCCL transport between the pack
+        and scatter phases, which runs on more than one GPU and is not part
+        of this single-GPU library."""
+        if group_size <= 1:
+            return
+        raise NotImplementedError(
+            "kv_exchange across instances needs RCCL send/recv between kv_exchange_pack and "
+            "kv_exchange_scatter; only the single-GPU pack/scatter phases are provided")

@@ -1,0 +1,56 @@
+"""Shared helpers of the GPU parity tests (checkers only)."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from kunserve_amd import KVPool, PageTable
+
+ATOL = 2e-3   # max-abs tolerance for fp16 attention outputs, fp32 accumulation
+
+
+def random_pool(num_pages, num_layers, num_kv_heads, page_size, head_dim, device, seed,
+                scale=1.0) -> KVPool:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    pool = KVPool.allocate(num_pages, num_layers, num_kv_heads, page_size, head_dim, device)
+    for t in (pool.k, pool.v):
+        # fill layer by layer to bound the temporary fp32 buffer
+        for layer in range(num_layers):
+            t[:, layer].copy_((torch.randn(t[:, layer].shape, generator=g, device=device,
+                                           dtype=torch.float32) * scale).to(torch.float16))
+    return pool
+
+
+def random_tensor(shape, device, seed, scale=1.0) -> torch.Tensor:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=device) * scale).to(torch.float16)
+
+
+def compact_for_oracle(pool: KVPool, layer: int, indptr: np.ndarray, indices: np.ndarray,
+                       rows=None):
+    """Host copies of only the pages the selected rows use (one layer), with
+    the table renumbered into the compact pool: keeps oracle inputs small
+    when the device pool is many GiB."""
+    rows = np.arange(len(indptr) - 1) if rows is None else np.asarray(rows)
+    pages = [indices[indptr[b]:indptr[b + 1]] for b in rows]
+    used = np.concatenate(pages) if pages else np.zeros(0, np.int64)
+    uniq, inv = np.unique(used, return_inverse=True)
+    sel = torch.from_numpy(uniq.astype(np.int64)).to(pool.device)
+    k = pool.k[:, layer].index_select(0, sel)[:, None].cpu().numpy()
+    v = pool.v[:, layer].index_select(0, sel)[:, None].cpu().numpy()
+    new_indptr = np.zeros(len(rows) + 1, dtype=np.int64)
+    np.cumsum([len(p) for p in pages], out=new_indptr[1:])
+    return k, v, new_indptr, inv.astype(np.int64)
+
+
+def table_from_csr(indptr, indices, kv_len, device) -> PageTable:
+    return PageTable(np.asarray(indptr, np.int32), np.asarray(indices, np.int32),
+                     np.asarray(kv_len, np.int32), device)
+
+
+def max_abs(a, b) -> float:
+    a = a.float().cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
+    b = b.float().cpu().numpy() if isinstance(b, torch.Tensor) else np.asarray(b)
+    return float(np.max(np.abs(a.astype(np.float64) - b.astype(np.float64)))) if a.size else 0.0

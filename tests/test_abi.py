@@ -1,0 +1,104 @@
+"""The C ABI library loads and exports exactly what include/kunserve_hip.h
+declares; host-only entry points behave (no GPU needed)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from kunserve_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "kunserve_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kunserve_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert len(names) >= 14
+    lib = _lib.lib()
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_version_and_error_channel():
+    lib = _lib.lib()
+    assert lib.kunserve_version() == 100
+    assert lib.kunserve_last_error() == b""
+
+
+def test_decode_plan_covers_every_token_once():
+    rng = np.random.default_rng(0)
+    kv = rng.integers(0, 5000, 37).astype(np.int32)
+    kv[3] = 0
+    for hq, hkv in [(32, 32), (32, 8), (64, 8), (12, 4)]:
+        cap = _lib.lib().kunserve_decode_plan_bound(kv.ctypes.data, kv.size)
+        buf = np.zeros(cap, dtype=np.int32)
+        info = _lib.DecodePlanInfo()
+        _lib.call("kunserve_decode_plan", kv.ctypes.data, kv.size, hq, hkv, 256, 0,
+                  buf.ctypes.data, cap, ctypes.byref(info))
+        work = buf[:4 * info.num_work].reshape(-1, 4)
+        merges = buf[4 * info.num_work:info.plan_ints].reshape(-1, 4)
+        assert info.group_size in (1, 2, 4, 8) and (hq // hkv) % info.group_size == 0
+        covered = np.zeros(kv.size, dtype=np.int64)
+        lengths = work[:, 2] - work[:, 1]
+        assert np.all(np.diff(lengths) <= 0), "work is ordered longest first"
+        for seq, b, e, slot in work:
+            assert 0 <= b <= e <= kv[seq] and e - b <= info.part_tokens
+            covered[seq] += e - b
+        assert np.array_equal(covered, kv)
+        slots = sorted(work[work[:, 3] >= 0, 3].tolist())
+        assert slots == list(range(info.num_slots))
+        for seq, s0, n, _ in merges:
+            assert n > 1 and set(work[work[:, 0] == seq, 3]) == set(range(s0, s0 + n))
+        single = [s for s in range(kv.size) if s not in set(merges[:, 0])]
+        assert all((work[work[:, 0] == s, 3] == -1).all() for s in single)
+
+
+def test_decode_plan_rejects_bad_arguments():
+    kv = np.array([10, 20], dtype=np.int32)
+    buf = np.zeros(64, dtype=np.int32)
+    info = _lib.DecodePlanInfo()
+    with pytest.raises(_lib.KunserveError, match="multiple"):
+        _lib.call("kunserve_decode_plan", kv.ctypes.data, 2, 30, 8, 256, 0, buf.ctypes.data,
+                  64, ctypes.byref(info))
+    with pytest.raises(_lib.KunserveError, match="part_tokens"):
+        _lib.call("kunserve_decode_plan", kv.ctypes.data, 2, 8, 8, 256, 100, buf.ctypes.data,
+                  64, ctypes.byref(info))
+    with pytest.raises(_lib.KunserveError) as e:
+        _lib.call("kunserve_decode_plan", kv.ctypes.data, 2, 8, 8, 256, 0, buf.ctypes.data, 2,
+                  ctypes.byref(info))
+    assert e.value.code == _lib.ENOSPC
+
+
+def test_prefill_plan_tiles():
+    q_indptr = np.array([0, 300, 301, 301 + 512], dtype=np.int32)
+    kv = np.array([1000, 1, 512], dtype=np.int32)
+    buf = np.zeros(64, dtype=np.int32)
+    info = _lib.PrefillPlanInfo()
+    _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, kv.ctypes.data, 3, buf.ctypes.data,
+              64, ctypes.byref(info))
+    tiles = buf[:info.plan_ints].reshape(-1, 2)
+    assert info.tile_q == 128
+    want = {(0, 0), (0, 128), (0, 256), (1, 0), (2, 0), (2, 128), (2, 256), (2, 384)}
+    assert set(map(tuple, tiles.tolist())) == want and len(tiles) == len(want)
+    bad = np.array([5, 1, 512], dtype=np.int32)   # kv_len shorter than q_len
+    with pytest.raises(_lib.KunserveError):
+        _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, bad.ctypes.data, 3,
+                  buf.ctypes.data, 64, ctypes.byref(info))
+
+
+def test_swap_rejects_out_of_range_ids_before_any_copy():
+    src = np.array([0, 9], dtype=np.int64)
+    dst = np.array([1, 2], dtype=np.int64)
+    dummy = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    with pytest.raises(_lib.KunserveError) as e:
+        _lib.call("kunserve_swap_blocks", src.ctypes.data, dst.ctypes.data, 2, 0, dummy, dummy,
+                  4, dummy, dummy, 8, 1024, None)
+    assert e.value.code == _lib.ERANGE

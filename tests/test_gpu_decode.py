@@ -1,0 +1,159 @@
+"""Paged decode attention on the GPU vs the CPU oracle (max-abs <= 2e-3)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from kunserve_amd import DecodePlan, paged_decode, workloads
+from oracle import paged_attention_ref as ref
+
+from helpers import ATOL, compact_for_oracle, max_abs, random_pool, random_tensor, table_from_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def run_decode(pool, layer, indptr, indices, kv_len, hq, device, seed, part_tokens=0,
+               q_scale=1.0):
+    table = table_from_csr(indptr, indices, kv_len, device)
+    q = random_tensor((len(kv_len), hq, pool.head_dim), device, seed, q_scale)
+    plan = DecodePlan(kv_len, hq, pool.num_kv_heads, device, part_tokens=part_tokens)
+    out = paged_decode(pool, layer, table, q, plan)
+    torch.cuda.synchronize()
+    return q, out, plan
+
+
+def oracle_decode(pool, layer, indptr, indices, kv_len, q, rows=None):
+    rows = np.arange(len(kv_len)) if rows is None else np.asarray(rows)
+    k, v, ip, ix = compact_for_oracle(pool, 0 if pool.num_layers == 1 else layer, indptr,
+                                      indices, rows)
+    qn = q[torch.from_numpy(rows).to(q.device)].cpu().numpy()
+    return ref.decode_attention(qn, k, v, 0, ip, ix, np.asarray(kv_len)[rows],
+                                1.0 / math.sqrt(pool.head_dim))
+
+
+def test_single_layer_decode_b8(device):
+    w = workloads.single_layer_decode()
+    s = 1.0 / math.sqrt(128)
+    pool = random_pool(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device, 11, s)
+    indptr, indices = w.csr()
+    q, out, _ = run_decode(pool, 0, indptr, indices, w.kv_len, w.num_qo_heads, device, 12, 0, s)
+    want = oracle_decode(pool, 0, indptr, indices, w.kv_len, q)
+    assert max_abs(out, want) <= ATOL
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (16, 2), (16, 1), (12, 4), (64, 8)])
+def test_decode_heads_and_dims(device, head_dim, hq, hkv):
+    rng = np.random.default_rng(hq * 1000 + hkv * 10 + head_dim)
+    ps, npg = 16, 600
+    kv = np.array([1, 2, 15, 16, 17, 100, 255, 256, 257, 700, 1500], dtype=np.int32)
+    need = (kv + ps - 1) // ps
+    perm = rng.permutation(npg)
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    indices = perm[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 2, hkv, ps, head_dim, device, 21)
+    q, out, _ = run_decode(pool, 1, indptr, indices, kv, hq, device, 22)
+    want = oracle_decode(pool, 1, indptr, indices, kv, q)
+    assert max_abs(out, want) <= ATOL
+
+
+@pytest.mark.parametrize("ps", [4, 8, 32, 256])
+def test_decode_page_sizes(device, ps):
+    rng = np.random.default_rng(ps)
+    kv = np.array([1, 3, 31, 64, 513, 2049], dtype=np.int32)
+    need = (kv + ps - 1) // ps
+    npg = int(need.sum()) + 7
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, 4, ps, 128, device, 31)
+    q, out, _ = run_decode(pool, 0, indptr, indices, kv, 8, device, 32)
+    want = oracle_decode(pool, 0, indptr, indices, kv, q)
+    assert max_abs(out, want) <= ATOL
+
+
+def test_decode_empty_and_zero_length_rows(device):
+    pool = random_pool(8, 1, 2, 16, 128, device, 41)
+    indptr = np.array([0, 0, 1, 1], dtype=np.int32)
+    indices = np.array([5], dtype=np.int32)
+    kv = np.array([0, 9, 0], dtype=np.int32)
+    q, out, _ = run_decode(pool, 0, indptr, indices, kv, 2, device, 42)
+    want = oracle_decode(pool, 0, indptr, indices, kv, q)
+    assert max_abs(out, want) <= ATOL
+    assert torch.all(out[0] == 0) and torch.all(out[2] == 0)
+    # no rows at all
+    plan = DecodePlan(np.zeros(0, np.int32), 2, 2, device)
+    assert plan.info.num_work == 0
+
+
+def test_decode_split_invariance(device):
+    """The result does not depend on the partition length (split-K + merge)."""
+    rng = np.random.default_rng(5)
+    kv = rng.integers(1, 9000, 24).astype(np.int32)
+    need = (kv + 15) // 16
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    npg = int(indptr[-1]) + 5
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, 8, 16, 128, device, 51)
+    outs = []
+    for part in (256, 512, 2048, 4096):
+        _, out, plan = run_decode(pool, 0, indptr, indices, kv, 32, device, 52, part)
+        assert plan.info.part_tokens == part
+        outs.append(out.float())
+    for o in outs[1:]:
+        assert max_abs(o, outs[0]) <= 1e-3
+    q = random_tensor((len(kv), 32, 128), device, 52)
+    rows = np.argsort(kv)[-4:]
+    want = oracle_decode(pool, 0, indptr, indices, kv, q, rows)
+    assert max_abs(outs[0][torch.from_numpy(rows).to(device)], want) <= ATOL
+
+
+def test_decode_page_permutation_bit_exact(device):
+    """Moving pages (and the table with them) does not change one bit."""
+    rng = np.random.default_rng(6)
+    kv = np.array([40, 333, 1024], dtype=np.int32)
+    need = (kv + 15) // 16
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    npg = 200
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, 4, 16, 128, device, 61)
+    q, out, _ = run_decode(pool, 0, indptr, indices, kv, 4, device, 62)
+    perm = rng.permutation(npg)
+    pk, pv = torch.empty_like(pool.k), torch.empty_like(pool.v)
+    idx = torch.from_numpy(perm).to(device)
+    pk[idx], pv[idx] = pool.k, pool.v
+    from kunserve_amd import KVPool
+    moved = KVPool(pk, pv)
+    _, out2, _ = run_decode(moved, 0, indptr, perm[indices].astype(np.int32), kv, 4, device, 62)
+    assert torch.equal(out, out2)
+
+
+def test_llama2_7b_decode_all_layers_sampled(device):
+    """Full Llama-2-7B decode shape (32 layers, 16384-page pool, batch 64);
+    every layer is checked on a sample of rows, always including the
+    longest and the shortest."""
+    w = workloads.llama2_7b_decode()
+    pool = random_pool(w.num_pages, w.num_layers, w.num_kv_heads, w.page_size, w.head_dim,
+                       device, 71)
+    indptr, indices = w.csr()
+    table = table_from_csr(indptr, indices, w.kv_len, device)
+    plan = DecodePlan(w.kv_len, w.num_qo_heads, w.num_kv_heads, device)
+    order = np.argsort(w.kv_len)
+    rows = np.unique(np.concatenate([order[:2], order[-2:], order[::16]]))
+    for layer in (0, 13, 31):
+        q = random_tensor((w.batch, w.num_qo_heads, w.head_dim), device, 100 + layer)
+        out = paged_decode(pool, layer, table, q, plan)
+        want = oracle_decode(pool, layer, indptr, indices, w.kv_len, q, rows)
+        assert max_abs(out[torch.from_numpy(rows).to(device)], want) <= ATOL
+
+
+def test_llama3_8b_gqa_decode_sampled(device):
+    w = workloads.llama3_8b_gqa_decode()
+    pool = random_pool(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device, 81)
+    indptr, indices = w.csr()
+    q, out, plan = run_decode(pool, 0, indptr, indices, w.kv_len, w.num_qo_heads, device, 82)
+    assert plan.info.num_merge > 0 and plan.info.group_size == 4
+    order = np.argsort(w.kv_len)
+    rows = np.unique(np.concatenate([order[:2], order[-3:], order[::32]]))
+    want = oracle_decode(pool, 0, indptr, indices, w.kv_len, q, rows)
+    assert max_abs(out[torch.from_numpy(rows).to(device)], want) <= ATOL

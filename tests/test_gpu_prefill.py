@@ -1,0 +1,159 @@
+"""K/V append (bit-exact) and chunked-prefill attention (max-abs <= 2e-3)
+on the GPU vs the CPU oracle, plus the pforward attention stage."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from kunserve_amd import (AttentionStep, LlamaOp, PrefillPlan, append_kv, paged_decode,
+                          paged_prefill, workloads, DecodePlan)
+from oracle import paged_attention_ref as ref
+
+from helpers import ATOL, compact_for_oracle, max_abs, random_pool, random_tensor, table_from_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def make_rows(rng, q_lens, prefixes, ps, npg):
+    kv = np.asarray(prefixes) + np.asarray(q_lens)
+    need = (kv + ps - 1) // ps
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    q_indptr = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    return kv.astype(np.int32), indptr, indices, q_indptr
+
+
+def test_append_bit_exact(device):
+    rng = np.random.default_rng(0)
+    ps, npg, hkv, d = 16, 64, 4, 128
+    q_lens, prefixes = [5, 1, 40, 16], [0, 33, 7, 16]
+    kv, indptr, indices, q_indptr = make_rows(rng, q_lens, prefixes, ps, npg)
+    pool = random_pool(npg, 3, hkv, ps, d, device, 1)
+    k0, v0 = pool.k.cpu().numpy(), pool.v.cpu().numpy()
+    T = int(q_indptr[-1])
+    kn, vn = random_tensor((T, hkv, d), device, 2), random_tensor((T, hkv, d), device, 3)
+    table = table_from_csr(indptr, indices, kv, device)
+    append_kv(pool, 2, table, torch.from_numpy(q_indptr).to(device), kn, vn)
+    torch.cuda.synchronize()
+    ref.append_kv(k0, v0, 2, indptr, indices, kv, q_indptr, kn.cpu().numpy(), vn.cpu().numpy())
+    assert np.array_equal(pool.k.cpu().numpy().view(np.int16), k0.view(np.int16))
+    assert np.array_equal(pool.v.cpu().numpy().view(np.int16), v0.view(np.int16))
+
+
+def run_prefill(pool, layer, q_lens, kv, indptr, indices, q_indptr, hq, device, seed):
+    T = int(q_indptr[-1])
+    q = random_tensor((T, hq, pool.head_dim), device, seed)
+    table = table_from_csr(indptr, indices, kv, device)
+    plan = PrefillPlan(q_indptr, kv, device)
+    out = paged_prefill(pool, layer, table, torch.from_numpy(q_indptr).to(device), q, plan)
+    torch.cuda.synchronize()
+    return q, out
+
+
+def oracle_prefill(pool, layer, q, q_indptr, indptr, indices, kv):
+    k, v, ip, ix = compact_for_oracle(pool, layer, indptr, indices)
+    return ref.prefill_attention(q.cpu().numpy(), q_indptr, k, v, 0, ip, ix, kv,
+                                 1.0 / math.sqrt(pool.head_dim))
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (12, 4)])
+@pytest.mark.parametrize("ps", [16, 64])
+def test_prefill_matches_oracle(device, hq, hkv, ps):
+    rng = np.random.default_rng(hq + ps)
+    q_lens = [1, 5, 64, 127, 128, 129, 300, 512]
+    prefixes = [0, 17, 0, 100, 1000, 3, 64, 2048]
+    npg = 400 if ps == 16 else 120
+    kv, indptr, indices, q_indptr = make_rows(rng, q_lens, prefixes, ps, npg)
+    pool = random_pool(npg, 2, hkv, ps, 128, device, 5)
+    q, out = run_prefill(pool, 1, q_lens, kv, indptr, indices, q_indptr, hq, device, 6)
+    want = oracle_prefill(pool, 1, q, q_indptr, indptr, indices, kv)
+    assert max_abs(out, want) <= ATOL
+
+
+def test_prefill_one_token_rows_equal_decode(device):
+    """A one-token prefill row is a decode row (use_tensor_cores path)."""
+    rng = np.random.default_rng(7)
+    q_lens, prefixes = [1] * 6, [0, 15, 16, 300, 1000, 2047]
+    kv, indptr, indices, q_indptr = make_rows(rng, q_lens, prefixes, 16, 300)
+    pool = random_pool(300, 1, 8, 16, 128, device, 8)
+    q, out = run_prefill(pool, 0, q_lens, kv, indptr, indices, q_indptr, 8, device, 9)
+    table = table_from_csr(indptr, indices, kv, device)
+    dec = paged_decode(pool, 0, table, q, DecodePlan(kv, 8, 8, device))
+    assert max_abs(out, dec) <= 1e-3
+
+
+def test_chunked_prefill_workload_sampled(device):
+    """The 16-sequence chunked-prefill workload: every step appends its chunk
+    and attends; two steps are checked against the oracle in full."""
+    w = workloads.chunked_prefill()
+    pool = random_pool(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device, 10)
+    steps = w.steps()
+    checked = {0, len(steps) - 1}
+    for i, (rows, ql, kv) in enumerate(steps):
+        pages = [w.pages[r] for r in rows]
+        q_indptr = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
+        need = (kv + 15) // 16
+        indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+        indices = np.concatenate([p[:n] for p, n in zip(pages, need)]).astype(np.int32)
+        T = int(q_indptr[-1])
+        k_new = random_tensor((T, w.num_kv_heads, w.head_dim), device, 100 + i)
+        v_new = random_tensor((T, w.num_kv_heads, w.head_dim), device, 200 + i)
+        table = table_from_csr(indptr, indices, kv, device)
+        qi = torch.from_numpy(q_indptr).to(device)
+        append_kv(pool, 0, table, qi, k_new, v_new)
+        q = random_tensor((T, w.num_qo_heads, w.head_dim), device, 300 + i)
+        out = paged_prefill(pool, 0, table, qi, q, PrefillPlan(q_indptr, kv, device))
+        if i in checked:
+            want = oracle_prefill(pool, 0, q, q_indptr, indptr, indices, kv)
+            assert max_abs(out, want) <= ATOL
+
+
+def test_attention_step_mixed_batch(device):
+    """One pforward step with prefill and decode rows interleaved: append of
+    every row's new tokens, then decode and prefill attention."""
+    op = LlamaOp(256, 2, 8, 4, 16, 128, 1, 1, 8, 4096, 4096, 1, device)
+    op.pool.k.copy_(random_tensor(op.pool.k.shape, device, 1))
+    op.pool.v.copy_(random_tensor(op.pool.v.shape, device, 2))
+    rng = np.random.default_rng(3)
+    perm = rng.permutation(256)
+    # rows: prefill chunk (first=32, 100 tokens), decode (first=77), prefill (first=0, 20),
+    # decode (first=1)
+    first = [32, 77, 0, 1]
+    flags = [1, 0, 1, 0]
+    q_lens = [100, 1, 20, 1]
+    kv = [132, 77, 20, 1]
+    need = [(k + 15) // 16 for k in kv]
+    pages, at = [], 0
+    for n in need:
+        pages.append(perm[at:at + n + 1].tolist())   # one spare page, as the block manager may hold
+        at += n + 1
+    tokens = [list(range(n)) for n in q_lens]
+    step = op.pforward(4, sum(q_lens), 256, 0, 2, tokens, first, flags, pages, 0, [], [], 0)
+    T = sum(q_lens)
+    q = random_tensor((T, 8, 128), device, 4)
+    k = random_tensor((T, 4, 128), device, 5)
+    v = random_tensor((T, 4, 128), device, 6)
+    k_host, v_host = op.pool.k.cpu().numpy(), op.pool.v.cpu().numpy()
+    out = step.run(1, q, k, v)
+    torch.cuda.synchronize()
+    q_indptr = np.concatenate([[0], np.cumsum(q_lens)])
+    indptr = np.concatenate([[0], np.cumsum(need)])
+    indices = np.concatenate([p[:n] for p, n in zip(pages, need)])
+    ref.append_kv(k_host, v_host, 1, indptr, indices, np.array(kv), q_indptr, k.cpu().numpy(),
+                  v.cpu().numpy())
+    assert np.array_equal(op.pool.k.cpu().numpy().view(np.int16), k_host.view(np.int16))
+    want = ref.prefill_attention(q.cpu().numpy(), q_indptr, k_host, v_host, 1, indptr, indices,
+                                 np.array(kv), 1 / math.sqrt(128))
+    assert max_abs(out, want) <= ATOL
+    assert step.decode is not None and step.prefill is not None
+
+
+def test_pforward_validates_arguments(device):
+    op = LlamaOp(16, 1, 2, 2, 16, 128, 1, 1, 8, 64, 64, 1, device)
+    with pytest.raises(ValueError, match="pages"):
+        op.pforward(1, 1, 16, 0, 1, [[1]], [40], [0], [[1]], 0, [], [], 0)
+    with pytest.raises(IndexError):
+        op.pforward(1, 1, 16, 0, 1, [[1]], [3], [0], [[16]], 0, [], [], 0)
+    with pytest.raises(ValueError, match="num_tokens"):
+        op.pforward(1, 2, 16, 0, 1, [[1]], [3], [0], [[1]], 0, [], [], 0)

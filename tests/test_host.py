@@ -1,0 +1,76 @@
+"""Host-side logic of the shim: step arguments -> kv lengths and CSR tables."""
+import numpy as np
+import pytest
+
+from kunserve_amd import csr_from_lists, kv_lens_for_step
+from kunserve_amd import workloads
+from oracle import paged_attention_ref as ref
+
+
+def test_kv_lens_rule_matches_oracle():
+    rng = np.random.default_rng(0)
+    first = rng.integers(1, 5000, 50)
+    ql = rng.integers(1, 600, 50)
+    flag = rng.integers(0, 2, 50)
+    ql = np.where(flag == 0, 1, ql)
+    got = kv_lens_for_step(first, ql, flag)
+    assert np.array_equal(got, ref.kv_lens_for_step(first, ql, flag))
+    # use_tensor_cores flags every row as prefill (kunserve/request.py:667-670)
+    assert np.array_equal(kv_lens_for_step([9], [1], [1]), [10])
+    with pytest.raises(ValueError):
+        kv_lens_for_step([0], [3], [0])
+
+
+def test_csr_truncates_and_validates():
+    pages = [[5, 6, 7], [1], [2, 3]]
+    indptr, indices = csr_from_lists(pages, np.array([17, 16, 3]), 16, 8)
+    assert indptr.tolist() == [0, 2, 3, 4]
+    assert indices.tolist() == [5, 6, 1, 2]          # rows truncated to ceil(kv/16) pages
+    with pytest.raises(ValueError, match="needs 2"):
+        csr_from_lists([[1]], np.array([17]), 16, 8)
+    with pytest.raises(IndexError):
+        csr_from_lists([[8]], np.array([3]), 16, 8)
+    with pytest.raises(IndexError):
+        csr_from_lists([[-1]], np.array([3]), 16, 8)
+    indptr, indices = csr_from_lists([[], [4]], np.array([0, 1]), 16, 8)
+    assert indptr.tolist() == [0, 0, 1] and indices.tolist() == [4]
+
+
+def test_workloads_are_seeded_and_disjoint():
+    for make in (workloads.single_layer_decode, workloads.llama2_7b_decode,
+                 workloads.llama3_8b_gqa_decode):
+        a, b = make(), make()
+        assert np.array_equal(a.kv_len, b.kv_len)
+        indptr, indices = a.csr()
+        assert np.unique(indices).size == indices.size            # no page shared
+        assert indices.max() < a.num_pages
+        assert np.array_equal(np.diff(indptr), (a.kv_len + a.page_size - 1) // a.page_size)
+    w = workloads.llama2_7b_decode()
+    assert w.kv_len.min() >= 16 and w.kv_len.max() <= 4096
+    # sample median of 64 lognormal(ln 700, 1) draws: 700 within a few standard errors
+    assert 450 <= np.median(w.kv_len) <= 1100
+
+
+def test_prefill_steps_cover_each_prompt_once():
+    p = workloads.chunked_prefill()
+    done = np.zeros_like(p.prompt_len)
+    for rows, ql, kv in p.steps():
+        assert np.all(ql <= p.chunk) and np.all(ql >= 1)
+        assert np.array_equal(kv, p.prefix_len[rows] + done[rows] + ql)
+        done[rows] += ql
+    assert np.array_equal(done, p.prompt_len)
+    # causal flop count against a brute-force sum on a tiny case
+    tiny = workloads.PrefillShape("t", 2, 2, 4, 16, 8, np.array([5]), np.array([3]), 2, [], 0)
+    visible = sum(3 + i + 1 for i in range(5))
+    assert tiny.causal_flops() == 4 * 2 * 4 * visible
+
+
+def test_remap_tables_point_at_copies():
+    r = workloads.kv_remap()
+    src_set = set(r.src.tolist())
+    m = dict(zip(r.src.tolist(), r.dst.tolist()))
+    for a, b in zip(r.decode.pages, r.decode_remapped.pages):
+        assert [m.get(int(x), int(x)) for x in a] == b.tolist()
+    allp = np.concatenate(r.decode.pages)
+    assert not np.any((allp >= 8192) & (allp < 16384))
+    assert any(int(x) in src_set for x in allp)

@@ -1,0 +1,256 @@
+"""Pins the CPU oracle (oracle/paged_attention_ref.py) before it is trusted.
+
+Each check is chosen so that a plausible slip in the oracle (slot vs page
+index swapped, wrong scale, GQA head mapping h % Hkv instead of h // G, an
+off-by-one in the causal bound or in the first-index rule) fails one of
+them. The attention references are torch's scaled_dot_product_attention in
+float64 on dense K/V; the dense K/V are written into pages by a separate
+element loop, not by the oracle's gather.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import paged_attention_ref as ref
+
+
+def scatter_dense(dense_k, dense_v, num_pages, num_layers, layer, page_size, rng):
+    """Writes per-sequence dense K/V [Hkv, n, D] into random pages with an
+    explicit element loop; returns pools and CSR tables."""
+    hkv, d = dense_k[0].shape[0], dense_k[0].shape[2]
+    kp = rng.standard_normal((num_pages, num_layers, hkv, page_size, d))
+    vp = rng.standard_normal((num_pages, num_layers, hkv, page_size, d))
+    perm = rng.permutation(num_pages)
+    indptr, indices, at = [0], [], 0
+    for K, V in zip(dense_k, dense_v):
+        n = K.shape[1]
+        npg = (n + page_size - 1) // page_size
+        pages = perm[at:at + npg]
+        at += npg
+        for t in range(n):
+            page, slot = pages[t // page_size], t % page_size
+            for h in range(hkv):
+                kp[page, layer, h, slot, :] = K[h, t]
+                vp[page, layer, h, slot, :] = V[h, t]
+        indices.extend(pages.tolist())
+        indptr.append(len(indices))
+    return kp, vp, np.array(indptr), np.array(indices)
+
+
+def sdpa(q, k, v, causal=False, scale=None):
+    return F.scaled_dot_product_attention(torch.from_numpy(q), torch.from_numpy(k),
+                                          torch.from_numpy(v), is_causal=causal,
+                                          scale=scale).numpy()
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2)])
+def test_decode_matches_sdpa_on_dense(hq, hkv):
+    rng = np.random.default_rng(0)
+    d, ps, L, layer = 32, 4, 3, 1
+    lens = [1, 5, 13, 16]
+    dk = [rng.standard_normal((hkv, n, d)) for n in lens]
+    dv = [rng.standard_normal((hkv, n, d)) for n in lens]
+    kp, vp, indptr, indices = scatter_dense(dk, dv, 32, L, layer, ps, rng)
+    q = rng.standard_normal((len(lens), hq, d))
+    scale = 1 / math.sqrt(d)
+    out = ref.decode_attention(q, kp, vp, layer, indptr, indices, np.array(lens), scale)
+    g = hq // hkv
+    for b, n in enumerate(lens):
+        K = np.repeat(dk[b], g, axis=0)   # head h uses kv head h // g
+        V = np.repeat(dv[b], g, axis=0)
+        want = sdpa(q[b][:, None, :], K, V, scale=scale)[:, 0]
+        np.testing.assert_allclose(out[b], want, rtol=1e-12, atol=1e-12)
+
+
+def test_decode_closed_forms():
+    rng = np.random.default_rng(1)
+    d, ps, hkv = 16, 4, 2
+    lens = [1, 9]
+    dk = [rng.standard_normal((hkv, n, d)) for n in lens]
+    dv = [rng.standard_normal((hkv, n, d)) for n in lens]
+    kp, vp, indptr, indices = scatter_dense(dk, dv, 8, 1, 0, ps, rng)
+    q = rng.standard_normal((2, hkv, d))
+    out = ref.decode_attention(q, kp, vp, 0, indptr, indices, np.array(lens), 0.3)
+    # kv_len 1: the output is that token's V.
+    np.testing.assert_allclose(out[0], dv[0][:, 0], rtol=0, atol=1e-15)
+    # q = 0: uniform weights, the output is the mean of V.
+    out0 = ref.decode_attention(np.zeros_like(q), kp, vp, 0, indptr, indices, np.array(lens), 0.3)
+    np.testing.assert_allclose(out0[1], dv[1].mean(axis=1), rtol=1e-13, atol=1e-13)
+    # kv_len 0 yields zeros.
+    z = ref.decode_attention(q[:1], kp, vp, 0, np.array([0, 0]), np.array([], dtype=int),
+                             np.array([0]), 0.3)
+    assert np.all(z == 0)
+
+
+def test_decode_page_permutation_invariance():
+    rng = np.random.default_rng(2)
+    d, ps, hkv, npg = 8, 4, 2, 16
+    kp = rng.standard_normal((npg, 1, hkv, ps, d))
+    vp = rng.standard_normal((npg, 1, hkv, ps, d))
+    indptr = np.array([0, 3, 7])
+    indices = rng.permutation(npg)[:7]
+    kv = np.array([10, 14])
+    q = rng.standard_normal((2, hkv, d))
+    base = ref.decode_attention(q, kp, vp, 0, indptr, indices, kv, 0.5)
+    perm = rng.permutation(npg)             # physical page p moves to perm[p]
+    kp2, vp2 = np.empty_like(kp), np.empty_like(vp)
+    kp2[perm], vp2[perm] = kp, vp
+    moved = ref.decode_attention(q, kp2, vp2, 0, indptr, perm[indices], kv, 0.5)
+    np.testing.assert_allclose(moved, base, rtol=0, atol=1e-15)
+
+
+def test_gqa_equals_repeated_mha():
+    rng = np.random.default_rng(3)
+    d, ps, hkv, g, npg = 8, 4, 2, 4, 12
+    kp = rng.standard_normal((npg, 1, hkv, ps, d))
+    vp = rng.standard_normal((npg, 1, hkv, ps, d))
+    indptr, indices, kv = np.array([0, 5]), rng.permutation(npg)[:5], np.array([18])
+    q = rng.standard_normal((1, hkv * g, d))
+    gqa = ref.decode_attention(q, kp, vp, 0, indptr, indices, kv, 0.4)
+    mha = ref.decode_attention(q, np.repeat(kp, g, axis=2), np.repeat(vp, g, axis=2), 0, indptr,
+                               indices, kv, 0.4)
+    np.testing.assert_allclose(gqa, mha, rtol=0, atol=1e-15)
+
+
+def test_prefill_without_prefix_matches_causal_sdpa():
+    rng = np.random.default_rng(4)
+    d, ps, h = 16, 4, 3
+    lens = [7, 12]
+    dk = [rng.standard_normal((h, n, d)) for n in lens]
+    dv = [rng.standard_normal((h, n, d)) for n in lens]
+    kp, vp, indptr, indices = scatter_dense(dk, dv, 16, 2, 1, ps, rng)
+    q_indptr = np.array([0, 7, 19])
+    q = rng.standard_normal((19, h, d))
+    out = ref.prefill_attention(q, q_indptr, kp, vp, 1, indptr, indices, np.array(lens), 0.25)
+    for b, n in enumerate(lens):
+        qb = q[q_indptr[b]:q_indptr[b + 1]].transpose(1, 0, 2)
+        want = sdpa(qb, dk[b], dv[b], causal=True, scale=0.25).transpose(1, 0, 2)
+        np.testing.assert_allclose(out[q_indptr[b]:q_indptr[b + 1]], want, rtol=1e-12,
+                                   atol=1e-12)
+
+
+def test_prefill_row_equals_decode_over_its_prefix():
+    rng = np.random.default_rng(5)
+    d, ps, hkv, g, npg = 8, 4, 2, 2, 20
+    kp = rng.standard_normal((npg, 1, hkv, ps, d))
+    vp = rng.standard_normal((npg, 1, hkv, ps, d))
+    indices = rng.permutation(npg)[:6]
+    kv, ql = 23, 5                    # prefix 18 cached, 5 new rows
+    q = rng.standard_normal((ql, hkv * g, d))
+    out = ref.prefill_attention(q, np.array([0, ql]), kp, vp, 0, np.array([0, 6]), indices,
+                                np.array([kv]), 0.3)
+    for i in range(ql):
+        dec = ref.decode_attention(q[i:i + 1], kp, vp, 0, np.array([0, 6]), indices,
+                                   np.array([kv - ql + i + 1]), 0.3)
+        np.testing.assert_allclose(out[i], dec[0], rtol=0, atol=1e-14)
+
+
+def _unique_pool(shape):
+    """int16 pool whose every element is distinct (mod 2^16), so a misplaced
+    element is visible."""
+    return (np.arange(np.prod(shape), dtype=np.int64) % 65521).astype(np.int16).reshape(shape)
+
+
+def test_append_matches_element_loop():
+    rng = np.random.default_rng(6)
+    npg, L, hkv, ps, d = 10, 2, 2, 4, 3
+    kp, vp = _unique_pool((npg, L, hkv, ps, d)), -_unique_pool((npg, L, hkv, ps, d))
+    indptr, indices = np.array([0, 3, 5]), np.array([7, 2, 9, 0, 4])
+    kv, q_indptr = np.array([10, 6]), np.array([0, 4, 5])
+    kn = rng.integers(-999, 999, (5, hkv, d)).astype(np.int16)
+    vn = rng.integers(-999, 999, (5, hkv, d)).astype(np.int16)
+    k1, v1 = kp.copy(), vp.copy()
+    ref.append_kv(k1, v1, 1, indptr, indices, kv, q_indptr, kn, vn)
+    k2, v2 = kp.copy(), vp.copy()
+    # row 0: positions 6..9 -> pages 2 (slots 2,3) and 9 (slots 0,1); row 1: position 5 -> page 4 slot 1
+    for tok, (page, slot) in enumerate([(2, 2), (2, 3), (9, 0), (9, 1), (4, 1)]):
+        for h in range(hkv):
+            for e in range(d):
+                k2[page, 1, h, slot, e] = kn[tok, h, e]
+                v2[page, 1, h, slot, e] = vn[tok, h, e]
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+
+
+def test_copy_swap_pack_scatter_match_element_loops():
+    shape = (12, 2, 2, 4, 3)
+    pool = _unique_pool(shape)
+    src, dst = [1, 5, 6], [9, 0, 11]
+    got = pool.copy()
+    ref.copy_blocks(got, src, dst)
+    want = pool.copy()
+    for s, t in zip(src, dst):
+        for idx in np.ndindex(shape[1:]):
+            want[(t,) + idx] = pool[(s,) + idx]
+    assert np.array_equal(got, want)
+
+    host = np.zeros((4,) + shape[1:], dtype=np.int16)
+    ref.swap([3, 7], [2, 0], pool, host)
+    assert np.array_equal(host[2], pool[3]) and np.array_equal(host[0], pool[7])
+    assert not host[1].any() and not host[3].any()
+
+    kp, vp = pool, -pool
+    scr = ref.kv_pack(kp, vp, 1, 2, [4, 8])
+    assert scr.shape == (1, 2, 2) + shape[2:]
+    for j, p in enumerate([4, 8]):
+        assert np.array_equal(scr[0, j, 0], kp[p, 1]) and np.array_equal(scr[0, j, 1], vp[p, 1])
+    k2, v2 = np.zeros_like(kp), np.zeros_like(vp)
+    ref.kv_scatter(k2, v2, 1, 2, [10, 3], scr)
+    assert np.array_equal(k2[10, 1], kp[4, 1]) and np.array_equal(v2[3, 1], vp[8, 1])
+    assert not k2[:, 0].any()
+
+
+class _Request:
+    """Lifecycle of a request restated from kunserve/request.py:368-462:
+    chunked prefill advances prefill_[begin|end]_index; after the prompt each
+    step decodes one token."""
+
+    def __init__(self, prompt_len, chunk):
+        self.prompt_len, self.chunk = prompt_len, chunk
+        self.begin = self.end = 0
+        self.outputs = 0
+
+    def context_stage(self):
+        return self.outputs == 0
+
+    def next_step(self):
+        """(first_token_index, q_len, flag, num_tokens for block allocation)."""
+        if self.context_stage():
+            self.begin = self.end
+            self.end = min(self.begin + self.chunk, self.prompt_len)
+            return self.begin, self.end - self.begin, 1, self.end
+
+    def finish_step(self):
+        if self.context_stage() and self.end < self.prompt_len:
+            return
+        self.outputs += 1
+
+
+def test_kv_len_rule_against_request_lifecycle():
+    req = _Request(prompt_len=37, chunk=16)
+    positions = []
+    for _ in range(8):
+        if req.context_stage():
+            first, ql, flag, _ = req.next_step()
+        else:
+            first, ql, flag = req.prompt_len + req.outputs, 1, 0
+        kv = int(ref.kv_lens_for_step([first], [ql], [flag])[0])
+        positions.extend(range(kv - ql, kv))
+        # blocks allocated for the step (kunserve/block_manager.py:493-500) cover kv_len
+        num_tokens = req.end if flag else req.prompt_len + req.outputs
+        assert kv <= num_tokens
+        req.finish_step()
+    # Every token position is appended exactly once, in order.
+    assert positions == list(range(len(positions)))
+
+
+def test_fused_page_ids():
+    # P = 4 base pages, 3 instances: page 1 -> {1, 5, 9}; extend ids follow 12.
+    assert ref.fused_page_ids(1, 4, 3) == [1, 5, 9]
+    assert ref.extend_page_ids(12, 3) == [12, 13, 14]
+    # instance rank 2 keeps fused id 8 + b
+    assert ref.kept_page_id(3, 12, 3, 2) == 11
+    # the kept id is one of the fused ids of that page
+    assert ref.kept_page_id(3, 12, 3, 2) in ref.fused_page_ids(3, 4, 3)
