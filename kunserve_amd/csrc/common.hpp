@@ -117,6 +117,10 @@ __device__ __forceinline__ float fast_exp2(float x) {
 __device__ __forceinline__ f16x8 load_f16x8(const f16* p) {
   return *reinterpret_cast<const f16x8*>(p);
 }
+// Non-temporal 16-byte load for data that is streamed once.
+__device__ __forceinline__ f16x8 load_f16x8_nt(const f16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p));
+}
 __device__ __forceinline__ void store_f16x8(f16* p, f16x8 v) {
   *reinterpret_cast<f16x8*>(p) = v;
 }

@@ -107,38 +107,44 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
   const f16* vb = a.v + int64_t(hkv) * a.head_stride + col * 8;
   const int nchunks = (te - tb + CHUNK - 1) / CHUNK;
 
-  for (int c = wave; c < nchunks; c += kWaves) {
-    const int t0 = tb + c * CHUNK;
-    f16x8 kr[kLoadsPerChunk], vr[kLoadsPerChunk];
+  // One chunk = kLoadsPerChunk token rows per lane, K and V. Loads are
+  // non-temporal: every K/V byte is read once, so it should not displace
+  // the page table and q in the caches.
+  struct Chunk {
+    f16x8 k[kLoadsPerChunk], v[kLoadsPerChunk];
     bool ok[kLoadsPerChunk];
+  };
+  auto load_chunk = [&](int c, Chunk& ch) {
+    const int t0 = tb + c * CHUNK;
 #pragma unroll
     for (int i = 0; i < kLoadsPerChunk; ++i) {
       const int t = t0 + i * TPL + row;
-      const int p = t < te ? s_pages[(t >> a.page_shift) - pb] : -1;
-      ok[i] = p >= 0;
+      const int p = (c < nchunks && t < te) ? s_pages[(t >> a.page_shift) - pb] : -1;
+      ch.ok[i] = p >= 0;
       const int64_t off = int64_t(p) * a.page_stride + int64_t(t & page_mask) * a.token_stride;
-      if (ok[i]) {
-        kr[i] = load_f16x8(kb + off);
-        vr[i] = load_f16x8(vb + off);
+      if (ch.ok[i]) {
+        ch.k[i] = load_f16x8_nt(kb + off);
+        ch.v[i] = load_f16x8_nt(vb + off);
       } else {
-        kr[i] = f16x8{};
-        vr[i] = f16x8{};
+        ch.k[i] = f16x8{};
+        ch.v[i] = f16x8{};
       }
     }
+  };
+  auto consume = [&](const Chunk& ch) {
     float vf[kLoadsPerChunk][8];
 #pragma unroll
     for (int i = 0; i < kLoadsPerChunk; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vf[i][j] = float(vr[i][j]);
-
+      for (int j = 0; j < 8; ++j) vf[i][j] = float(ch.v[i][j]);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float s[kLoadsPerChunk];
       float mx = m[g];
 #pragma unroll
       for (int i = 0; i < kLoadsPerChunk; ++i) {
-        s[i] = group_sum<LPT>(dot8(qv[g], kr[i], 0.f)) * a.scale_log2;
-        s[i] = ok[i] ? s[i] : -INFINITY;
+        s[i] = group_sum<LPT>(dot8(qv[g], ch.k[i], 0.f)) * a.scale_log2;
+        s[i] = ch.ok[i] ? s[i] : -INFINITY;
         mx = fmaxf(mx, s[i]);
       }
       const float alpha = fast_exp2(m[g] - mx);
@@ -158,6 +164,24 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
         for (int i = 0; i < kLoadsPerChunk; ++i) x = fmaf(p[i], vf[i][j], x);
         acc[g][j] = x;
       }
+    }
+  };
+
+  // Software pipeline over this wave's chunks (wave, wave + 4, ...): the
+  // loads of the next chunk are in flight while the current one is reduced.
+  if (wave < nchunks) {
+    Chunk c0, c1;
+    int c = wave;
+    load_chunk(c, c0);
+    while (true) {
+      load_chunk(c + kWaves, c1);
+      consume(c0);
+      c += kWaves;
+      if (c >= nchunks) break;
+      load_chunk(c + kWaves, c0);
+      consume(c1);
+      c += kWaves;
+      if (c >= nchunks) break;
     }
   }
 
@@ -218,30 +242,51 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-// Combines the partitions of split sequences: one workgroup per
-// (sequence, q head), one thread per dimension.
+// Combines the partitions of split sequences: one wave per (sequence,
+// q head). Lane j first reads the log-sum-exp of partition j, so the
+// weights come from one round of loads; each lane then accumulates D/64
+// dimensions over the partitions.
 template <int D>
-__global__ __launch_bounds__(D) void decode_merge_kernel(const int32_t* merges,
-                                                         const float* part_o,
-                                                         const float* part_lse, f16* out,
-                                                         int64_t o_tok, int64_t o_head,
-                                                         int32_t num_qo_heads) {
+__global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merges,
+                                                             const float* part_o,
+                                                             const float* part_lse, f16* out,
+                                                             int64_t o_tok, int64_t o_head,
+                                                             int32_t num_qo_heads) {
+  constexpr int DPL = D / kWave;
   const int32_t* mg = merges + 4 * blockIdx.x;
   const int seq = mg[0], s0 = mg[1], n = mg[2];
   const int hq = blockIdx.y;
-  const int d = threadIdx.x;
+  const int lane = threadIdx.x;
+
   float mx = -INFINITY;
-  for (int j = 0; j < n; ++j) mx = fmaxf(mx, part_lse[int64_t(s0 + j) * num_qo_heads + hq]);
-  float wsum = 0.f, o = 0.f;
+  for (int j = lane; j < n; j += kWave)
+    mx = fmaxf(mx, part_lse[int64_t(s0 + j) * num_qo_heads + hq]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+
+  float o[DPL] = {};
+  float wsum = 0.f;
   if (mx > -INFINITY) {
-    for (int j = 0; j < n; ++j) {
-      const int64_t sj = int64_t(s0 + j) * num_qo_heads + hq;
-      const float f = fast_exp2(part_lse[sj] - mx);
-      wsum += f;
-      o += f * part_o[sj * D + d];
+    for (int base = 0; base < n; base += kWave) {
+      const int j = base + lane;
+      const float w = j < n ? fast_exp2(part_lse[int64_t(s0 + j) * num_qo_heads + hq] - mx) : 0.f;
+      wsum += w;
+      const int cnt = min(kWave, n - base);
+#pragma unroll 4
+      for (int t = 0; t < cnt; ++t) {
+        const float wt = __shfl(w, t);
+        const float* src = part_o + (int64_t(s0 + base + t) * num_qo_heads + hq) * D + lane * DPL;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) o[e] = fmaf(wt, src[e], o[e]);
+      }
     }
   }
-  out[int64_t(seq) * o_tok + int64_t(hq) * o_head + d] = f16(wsum > 0.f ? o / wsum : 0.f);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) wsum += __shfl_xor(wsum, off);
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  f16* dst = out + int64_t(seq) * o_tok + int64_t(hq) * o_head + lane * DPL;
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) dst[e] = f16(o[e] * inv);
 }
 
 int pick_group(int ratio) {
@@ -268,7 +313,7 @@ template <int D>
 int launch_merge(const int32_t* merges, int num_merge, const float* po, const float* pl, f16* out,
                  int64_t o_tok, int64_t o_head, int hq, hipStream_t s) {
   dim3 grid(num_merge, hq);
-  decode_merge_kernel<D><<<grid, D, 0, s>>>(merges, po, pl, out, o_tok, o_head, hq);
+  decode_merge_kernel<D><<<grid, kWave, 0, s>>>(merges, po, pl, out, o_tok, o_head, hq);
   KSV_CHECK_LAUNCH();
   return KUNSERVE_OK;
 }
@@ -303,19 +348,16 @@ extern "C" int kunserve_decode_plan(const int32_t* kv_len_host, int32_t num_seqs
   const int64_t head_groups = num_qo_heads / group;
 
   if (part_tokens == 0) {
-    // Largest partition that still gives >= 8 workgroups per CU; short
-    // batches fall back to the minimum partition.
-    const int64_t target = int64_t(std::max(num_cus, 1)) * 8;
+    // Aim for ~8 partitions per CU over the whole grid: the largest
+    // power-of-two partition not above (total tokens x head groups) /
+    // (8 x CUs). Long rows are then split finely enough that the longest
+    // work item is a small fraction of the launch, while short batches
+    // keep whole rows (no merge pass).
+    int64_t total = 0;
+    for (int32_t b = 0; b < num_seqs; ++b) total += kv_len_host[b];
+    const int64_t per = total * head_groups / (int64_t(std::max(num_cus, 1)) * 8);
     part_tokens = kMinPartTokens;
-    for (int cand = kMaxPartTokens; cand >= kMinPartTokens; cand >>= 1) {
-      int64_t wgs = 0;
-      for (int32_t b = 0; b < num_seqs; ++b)
-        wgs += std::max<int64_t>(1, ceil_div(kv_len_host[b], cand));
-      if (wgs * head_groups >= target) {
-        part_tokens = cand;
-        break;
-      }
-    }
+    while (part_tokens * 2 <= std::min<int64_t>(per, kMaxPartTokens)) part_tokens *= 2;
   }
   KSV_CHECK_ARG(part_tokens >= kMinPartTokens && part_tokens <= kMaxPartTokens &&
                     part_tokens % 64 == 0,
