@@ -213,7 +213,7 @@ def bench_prefill(args, device):
         T = int(q_indptr[-1])
         table = ks.PageTable(indptr, indices, kv, device)
         qi = torch.from_numpy(q_indptr).to(device)
-        plan = ks.PrefillPlan(q_indptr, kv, device)
+        plan = ks.PrefillPlan(q_indptr, kv, w.num_qo_heads, w.num_kv_heads, device)
         mk = lambda h: torch.randn((T, h, w.head_dim), generator=gen, device=device).half()
         steps.append((table, qi, plan, mk(w.num_qo_heads), mk(w.num_kv_heads),
                       mk(w.num_kv_heads), torch.empty((T, w.num_qo_heads, w.head_dim),
@@ -239,6 +239,8 @@ def bench_prefill(args, device):
     timer = LaunchTimer()
     run(timer)
     attn_ms = timer.mean_ms() * len(steps)
+    per_step = [a.elapsed_time(b) for a, b in timer.pairs]
+    log("prefill per-step attention ms: " + ", ".join(f"{t:.3f}" for t in per_step))
     flops = w.causal_flops()
     tflops = flops / (attn_ms * 1e-3) / 1e12
     log(f"prefill: {len(steps)} chunk steps, {elapsed * 1e3:.3f} ms with append; attention "

@@ -197,15 +197,23 @@ int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer,
 /* ------------------------------------- chunked-prefill attention (A5 ii) */
 
 typedef struct {
-  int32_t num_tiles;     /* (row, q-tile) work items                       */
+  int32_t num_tiles;     /* workgroups of the launch (incl. padding)        */
   int32_t tile_q;        /* q rows per tile                                */
-  int32_t plan_ints;
+  int32_t plan_ints;     /* int32 entries of the plan buffer in use       */
+  int32_t num_qo_heads;  /* heads the plan was made for                    */
 } kunserve_prefill_plan_info;
 
+/* Upper bound of the prefill plan length (int32 entries). */
+int64_t kunserve_prefill_plan_bound(const int32_t* q_indptr_host,
+                                    int32_t num_seqs, int32_t num_qo_heads);
+
 /* Host-side plan: tiles the ragged q rows (q_len[b] = q_indptr[b+1] -
- * q_indptr[b]) into tiles of tile_q rows. */
+ * q_indptr[b]) of every q head into tiles of tile_q rows, and orders the
+ * (row, tile, head) items so that items reading the same K/V (same row and
+ * KV head) run back to back on one XCD (one L2), longest first. */
 int kunserve_prefill_plan(const int32_t* q_indptr_host,
                           const int32_t* kv_len_host, int32_t num_seqs,
+                          int32_t num_qo_heads, int32_t num_kv_heads,
                           int32_t* plan_host, int64_t plan_capacity,
                           kunserve_prefill_plan_info* info);
 

@@ -6,17 +6,22 @@
 //
 // Attention: flash-attention style on fp16 MFMA (v_mfma_f32_32x32x16_f16,
 // gfx950), fp32 accumulation and online softmax.
-//  * Workgroup = 4 waves = 128 query rows of one (sequence, q head); each
-//    wave owns 32 rows. The grid walks (q tile, head).
-//  * K/V tiles of 64 tokens are gathered from pages into LDS (K row-major,
-//    V transposed), both with XOR swizzles so that the MFMA operand reads
-//    (ds_read_b128 for K, ds_read_b64 for V^T) and the staging writes are
-//    free of bank conflicts.
+//  * Workgroup = 8 waves = 256 query rows of one (sequence, q head); each
+//    wave owns 32 rows. Two waves share a SIMD, so one wave's softmax
+//    (VALU, exp) overlaps the other's MFMAs.
+//  * K/V tiles of 64 tokens are gathered from pages into double-buffered
+//    LDS (K row-major, V transposed), both with XOR swizzles so that the
+//    MFMA operand reads (ds_read_b128 for K, ds_read_b64 for V^T) and the
+//    staging writes are free of bank conflicts. The next tile's global
+//    loads are issued before the current tile's math, so their latency
+//    hides behind it; one barrier per tile.
 //  * S^T = K.Q^T is computed so that the accumulator layout (one query row
 //    per lane column) is directly the B operand of O^T = V^T.P^T: the
 //    probabilities never leave registers.
-//  * Causal masking is applied per element; tiles entirely past a wave's
-//    last visible position are skipped.
+//  * Causal masking only on tiles that cross a wave's diagonal; tiles past
+//    a wave's last visible position skip the math.
+//  * The plan places the workgroups that read the same K/V (same sequence
+//    and KV head) back to back on one XCD so that they share its L2.
 #include <algorithm>
 #include <vector>
 
@@ -25,10 +30,13 @@
 namespace kunserve {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kTileQ = 128;     // query rows per workgroup
-constexpr int kTileKV = 64;     // kv tokens per iteration
-constexpr int kD = 128;         // head_dim of the MFMA kernel
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kTileQ = 32 * kWaves;   // query rows per workgroup (256)
+constexpr int kTileKV = 64;           // kv tokens per iteration
+constexpr int kD = 128;               // head_dim of the MFMA kernel
+constexpr int kXcds = 8;              // MI355X: workgroup i runs on XCD i % 8
+constexpr int kLoadsPerThread = kTileKV * kD / 8 / kThreads;   // 16-byte K (and V) loads
 
 struct PrefillArgs {
   const f16* q;
@@ -44,20 +52,36 @@ struct PrefillArgs {
   const int32_t* indices;
   const int32_t* kv_len;
   const int32_t* q_indptr;
-  const int32_t* tiles;   // [num_tiles][2]: seq, first q row of the tile
+  const int32_t* tiles;   // [num_tiles][3]: seq (-1: padding), first q row, q head
   int32_t ratio;
   float scale_log2;
 };
 
-// LDS element offsets. K: [token][dim], 16-byte chunk index XOR (token & 15).
-__device__ __forceinline__ int sk_off(int t, int chunk) { return t * kD + ((chunk ^ (t & 15)) << 3); }
-// V^T: [dim][token], 4-token group index XOR g(dim).
-__device__ __forceinline__ int vt_swz(int d) { return ((d & 15) ^ (d >> 4)) & 15; }
-__device__ __forceinline__ int sv_off(int d, int group) { return d * kTileKV + ((group ^ vt_swz(d)) << 2); }
+// LDS layouts (element offsets within one buffer of kTileKV x kD halves;
+// the two buffers differ in bit 13, so buffer selection is an XOR too).
+// K: [token][dim], the 16-byte chunk index XORed with (token & 15).
+//    offset(t, chunk) = (t*128 | (t & 15) << 3) ^ (chunk << 3)
+__device__ __forceinline__ int sk_off(int t, int chunk) { return (t * kD | (t & 15) << 3) ^ (chunk << 3); }
+// V^T: [dim][token], tokens of each row stored in MFMA k-slot order: chunk
+// c = 2ks + h (8 halves) holds tokens 16ks + 4h + {0..3} and 16ks + 8 + 4h
+// + {0..3}, so one ds_read_b128 is one A operand. Chunk index XORed with
+// f(d) = (d ^ d >> 3) & 7.
+//    offset(d, c) = (d*64 | f(d) << 3) ^ (c << 3)
+__device__ __forceinline__ int vt_base(int d) { return d * kTileKV | ((d ^ (d >> 3)) & 7) << 3; }
+__device__ __forceinline__ int vt_tok(int t) {   // (chunk << 3) | position of token t
+  return ((2 * (t >> 4) + ((t >> 2) & 1)) << 3) | (((t >> 3) & 1) << 2) | (t & 3);
+}
+constexpr int kBufHalves = kTileKV * kD;   // 8192: bit 13
 
 __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) f16 sK[kTileKV * kD];
-  __shared__ __attribute__((aligned(16))) f16 sV[kD * kTileKV];
+  __shared__ __attribute__((aligned(16))) f16 sK[2 * kBufHalves];
+  __shared__ __attribute__((aligned(16))) f16 sV[2 * kBufHalves];
+
+  const int32_t* item = a.tiles + 3 * blockIdx.x;
+  const int seq = item[0];
+  if (seq < 0) return;   // padding workgroup (uniform: no barrier reached)
+  const int q0 = item[1];
+  const int hq = item[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -65,9 +89,6 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   const int r = lane & 31;       // query row within the wave / MFMA column
   const int h = lane >> 5;       // MFMA k-half
 
-  const int seq = a.tiles[2 * blockIdx.x];
-  const int q0 = a.tiles[2 * blockIdx.x + 1];
-  const int hq = blockIdx.y;
   const int hkv = hq / a.ratio;
   const int qb = a.q_indptr[seq];
   const int q_len = a.q_indptr[seq + 1] - qb;
@@ -80,8 +101,10 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   const bool row_ok = qrow < q_len;
   const int qpos = prefix + qrow;
   const bool wave_active = q0 + wave * 32 < q_len;
+  const int wave_first_pos = prefix + q0 + wave * 32;
   const int wave_last_pos = prefix + min(q0 + wave * 32 + 31, q_len - 1);
   const int kv_end = prefix + min(q0 + kTileQ, q_len);   // exclusive
+  const int ntiles = (kv_end + kTileKV - 1) / kTileKV;
 
   // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
   f16x8 qf[8];
@@ -94,62 +117,94 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   f32x16 o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = f32x16{};
-  float m = -1.0e30f, lsum = 0.f;
+  float m = -1.0e30f;   // running max of this row, in scaled (log2) units
+  float lsum = 0.f;     // this lane's share of the row sum (other half: lane ^ 32)
 
   const f16* kbase = a.k + int64_t(hkv) * a.head_stride;
   const f16* vbase = a.v + int64_t(hkv) * a.head_stride;
 
-  for (int n0 = 0; n0 < kv_end; n0 += kTileKV) {
-    __syncthreads();   // the previous tile has been consumed
+  f16x8 kr[kLoadsPerThread], vr[kLoadsPerThread];
+  auto fetch = [&](int n0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kLoadsPerThread; ++i) {
       const int c = tid + kThreads * i;
       const int t = c >> 4, dc = c & 15;
       const int tok = n0 + t;
-      f16x8 kv = f16x8{}, vv = f16x8{};
-      if (tok < kvl) {
-        const int p = pages[tok >> a.page_shift];
-        if (p >= 0 && p < a.num_pages) {
-          const int64_t off = int64_t(p) * a.page_stride + int64_t(tok & page_mask) * a.token_stride + dc * 8;
-          kv = load_f16x8(kbase + off);
-          vv = load_f16x8(vbase + off);
-        }
+      const int p = tok < kvl ? pages[tok >> a.page_shift] : -1;
+      if (p >= 0 && p < a.num_pages) {
+        const int64_t off =
+            int64_t(p) * a.page_stride + int64_t(tok & page_mask) * a.token_stride + dc * 8;
+        kr[i] = load_f16x8(kbase + off);
+        vr[i] = load_f16x8(vbase + off);
+      } else {
+        kr[i] = f16x8{};
+        vr[i] = f16x8{};
       }
-      *reinterpret_cast<f16x8*>(&sK[sk_off(t, dc)]) = kv;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sV[sv_off(dc * 8 + j, t >> 2) + (t & 3)] = vv[j];
     }
-    __syncthreads();
-    if (!wave_active || n0 > wave_last_pos) continue;
+  };
+  auto stash = [&](int buf) {
+    const int bo = buf * kBufHalves;
+#pragma unroll
+    for (int i = 0; i < kLoadsPerThread; ++i) {
+      const int c = tid + kThreads * i;
+      const int t = c >> 4, dc = c & 15;
+      *reinterpret_cast<f16x8*>(&sK[bo ^ sk_off(t, dc)]) = kr[i];
+      const int tv = vt_tok(t);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sV[bo ^ vt_base(dc * 8 + j) ^ tv] = vr[i][j];
+    }
+  };
 
+  // Per-lane LDS bases (buffer 0); every operand address is one XOR away.
+  const int kb0 = sk_off(r, h);            // K rows r (mt = 0) and r + 32 (^ 4096)
+  int vb[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) vb[dt] = vt_base(32 * dt + r) ^ (h << 3);
+
+  auto compute = [&](int buf, int n0) {
+    const int bo = buf * kBufHalves;
     // S^T tiles: rows = kv tokens 32*mt + i, columns = query rows.
     f32x16 st[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      st[mt] = f32x16{};
-      const int tk = 32 * mt + r;
+      const int kb = bo ^ kb0 ^ (mt << 12);
+      st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+          *reinterpret_cast<const f16x8*>(&sK[kb]), qf[0], f32x16{}, 0, 0, 0);
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const f16x8 ka = *reinterpret_cast<const f16x8*>(&sK[sk_off(tk, 2 * s + h)]);
+      for (int s = 1; s < 8; ++s) {
+        const f16x8 ka = *reinterpret_cast<const f16x8*>(&sK[kb ^ (s << 4)]);
         st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[s], st[mt], 0, 0, 0);
       }
     }
-
-    // Scale, mask, running max. Lane holds tokens 32mt + 8(v/4) + 4h + v%4.
-    float mx = m;
+    // Lane holds tokens n0 + 32mt + 8(v/4) + 4h + v%4 of query row r.
+    float mx = -INFINITY;
+    if (n0 + kTileKV - 1 > wave_first_pos || n0 + kTileKV > kvl) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int tok = n0 + 32 * mt + 8 * (v >> 2) + 4 * h + (v & 3);
-        float x = st[mt][v] * a.scale_log2;
-        x = (tok <= qpos && tok < kvl) ? x : -INFINITY;
-        st[mt][v] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float alpha = fast_exp2(m - mx);
-    m = mx;
+        for (int v = 0; v < 16; ++v) {
+          const int tok = n0 + 32 * mt + 8 * (v >> 2) + 4 * h + (v & 3);
+          if (tok > qpos || tok >= kvl) st[mt][v] = -INFINITY;
+          mx = fmaxf(mx, st[mt][v]);
+        }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, st[mt][v]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
+    // Lazy running max: move it only when the tile's max exceeds it by more
+    // than 8 (log2 units). Probabilities then stay <= 2^8 (exact in fp16 and
+    // fp32), and the O rescale is skipped unless some row of the wave moved.
+    if (__any(mx > m + 8.f)) {
+      const float m_new = mx > m + 8.f ? mx : m;
+      const float alpha = fast_exp2(m - m_new);
+      m = m_new;
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    }
 
     // P^T as B operands: k-step ks covers tokens 16ks + 4h + {0..3} and
     // 16ks + 8 + 4h + {0..3}, i.e. accumulator entries v = 8(ks%2) + e of tile ks/2.
@@ -159,26 +214,34 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float p = fast_exp2(st[mt][v] - mx);
+        const float p = fast_exp2(fmaf(st[mt][v], a.scale_log2, -m));
         ps += p;
         pb[2 * mt + (v >> 3)][v & 7] = f16(p);
       }
-    lsum = lsum * alpha + ps;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    lsum += ps;
 
     // O^T[dims, rows] += V^T[dims, tokens] . P^T[tokens, rows]
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const int d = 32 * dt + r;
-        const f16x4 lo = *reinterpret_cast<const f16x4*>(&sV[sv_off(d, 4 * ks + h)]);
-        const f16x4 hi = *reinterpret_cast<const f16x4*>(&sV[sv_off(d, 4 * ks + 2 + h)]);
-        const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const f16x8 va = *reinterpret_cast<const f16x8*>(&sV[bo ^ vb[dt] ^ (ks << 4)]);
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[ks], o[dt], 0, 0, 0);
       }
     }
+  };
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int it = 0; it < ntiles; ++it) {
+    const int n0 = it * kTileKV;
+    const int buf = it & 1;
+    const bool more = it + 1 < ntiles;
+    if (more) fetch(n0 + kTileKV);   // in flight during this tile's math
+    if (wave_active && n0 <= wave_last_pos) compute(buf, n0);
+    if (more) stash(buf ^ 1);        // that buffer was last read before the previous barrier
+    __syncthreads();
   }
 
   lsum += __shfl_xor(lsum, 32);
@@ -296,38 +359,92 @@ extern "C" int kunserve_append_kv(const kunserve_kv_pool* pool, int32_t layer,
   return KUNSERVE_OK;
 }
 
+extern "C" int64_t kunserve_prefill_plan_bound(const int32_t* q_indptr_host, int32_t num_seqs,
+                                               int32_t num_qo_heads) {
+  if (num_seqs < 0 || num_qo_heads <= 0 || (num_seqs > 0 && !q_indptr_host)) return -1;
+  int64_t tiles = 0;
+  for (int32_t b = 0; b < num_seqs; ++b)
+    tiles += (std::max(q_indptr_host[b + 1] - q_indptr_host[b], 0) + kTileQ - 1) / kTileQ;
+  // Worst case: every item on one XCD, the others padded to the same depth.
+  return 3 * kXcds * (tiles * num_qo_heads + 1);
+}
+
 extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t* kv_len_host,
-                                     int32_t num_seqs, int32_t* plan_host, int64_t plan_capacity,
-                                     kunserve_prefill_plan_info* info) {
+                                     int32_t num_seqs, int32_t num_qo_heads,
+                                     int32_t num_kv_heads, int32_t* plan_host,
+                                     int64_t plan_capacity, kunserve_prefill_plan_info* info) {
   clear_error();
   KSV_CHECK_ARG(info && plan_host && num_seqs >= 0, "bad argument");
+  KSV_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && num_qo_heads % num_kv_heads == 0,
+                "num_qo_heads %d not a multiple of num_kv_heads %d", num_qo_heads, num_kv_heads);
   if (num_seqs > 0) KSV_CHECK_ARG(q_indptr_host && kv_len_host, "null q_indptr / kv_len");
-  struct Tile { int32_t seq, q0; int64_t cost; };
-  std::vector<Tile> tiles;
+  const int ratio = num_qo_heads / num_kv_heads;
+  // A group = (sequence, KV head, q-tile range): its items (all `ratio` q
+  // heads of each tile) read the same K/V. Groups go to XCDs greedily, most
+  // work first. A (sequence, KV head) keeps all its tiles in one group
+  // unless there are too few groups to spread over the XCDs.
+  struct Group { int32_t seq, hkv, t0, t1; int64_t cost; };
+  int64_t n_pairs = 0;
   for (int32_t b = 0; b < num_seqs; ++b) {
     const int32_t ql = q_indptr_host[b + 1] - q_indptr_host[b];
     KSV_CHECK_ARG(ql >= 0, "q_indptr not monotone at %d", b);
     KSV_CHECK_ARG(kv_len_host[b] >= ql, "kv_len[%d] = %d < q_len %d", b, kv_len_host[b], ql);
-    const int32_t prefix = kv_len_host[b] - ql;
-    for (int32_t q0 = 0; q0 < ql; q0 += kTileQ)
-      tiles.push_back({b, q0, int64_t(prefix) + std::min(q0 + kTileQ, ql)});
+    if (ql > 0) n_pairs += num_kv_heads;
   }
-  // Most kv work first so that the longest tiles do not trail the grid.
-  std::stable_sort(tiles.begin(), tiles.end(),
-                   [](const Tile& x, const Tile& y) { return x.cost > y.cost; });
-  const int64_t need = 2 * int64_t(tiles.size());
+  const bool split_tiles = n_pairs < 2 * kXcds;
+  std::vector<Group> groups;
+  for (int32_t b = 0; b < num_seqs; ++b) {
+    const int32_t ql = q_indptr_host[b + 1] - q_indptr_host[b];
+    if (ql == 0) continue;
+    const int32_t prefix = kv_len_host[b] - ql;
+    auto tile_cost = [&](int32_t q0) {
+      return (int64_t(prefix) + std::min(q0 + kTileQ, ql)) * ratio;
+    };
+    for (int32_t g = 0; g < num_kv_heads; ++g) {
+      if (split_tiles) {
+        for (int32_t q0 = 0; q0 < ql; q0 += kTileQ)
+          groups.push_back({b, g, q0, std::min(q0 + kTileQ, ql), tile_cost(q0)});
+      } else {
+        int64_t cost = 0;
+        for (int32_t q0 = 0; q0 < ql; q0 += kTileQ) cost += tile_cost(q0);
+        groups.push_back({b, g, 0, ql, cost});
+      }
+    }
+  }
+  std::stable_sort(groups.begin(), groups.end(),
+                   [](const Group& x, const Group& y) { return x.cost > y.cost; });
+  std::vector<std::vector<int32_t>> lanes(kXcds);
+  int64_t load[kXcds] = {};
+  for (const Group& g : groups) {
+    const int x = int(std::min_element(load, load + kXcds) - load);
+    load[x] += g.cost;
+    for (int32_t q0 = g.t0; q0 < g.t1; q0 += kTileQ)
+      for (int32_t hq = g.hkv * ratio; hq < (g.hkv + 1) * ratio; ++hq)
+        lanes[x].insert(lanes[x].end(), {g.seq, q0, hq});
+  }
+  size_t depth = 0;
+  for (const auto& l : lanes) depth = std::max(depth, l.size() / 3);
+  const int64_t need = 3 * int64_t(depth) * kXcds;
   if (need > plan_capacity) {
     set_error("prefill plan needs %lld ints, capacity %lld", (long long)need,
               (long long)plan_capacity);
     return KUNSERVE_ENOSPC;
   }
-  for (size_t i = 0; i < tiles.size(); ++i) {
-    plan_host[2 * i] = tiles[i].seq;
-    plan_host[2 * i + 1] = tiles[i].q0;
-  }
-  info->num_tiles = int32_t(tiles.size());
+  // Workgroup L runs on XCD L % 8: item i of XCD x goes to L = 8 i + x.
+  for (size_t i = 0; i < depth; ++i)
+    for (int x = 0; x < kXcds; ++x) {
+      int32_t* dst = plan_host + 3 * (i * kXcds + x);
+      if (3 * i < lanes[x].size()) {
+        std::copy(lanes[x].begin() + 3 * i, lanes[x].begin() + 3 * i + 3, dst);
+      } else {
+        dst[0] = -1;
+        dst[1] = dst[2] = 0;
+      }
+    }
+  info->num_tiles = int32_t(depth * kXcds);
   info->tile_q = kTileQ;
   info->plan_ints = int32_t(need);
+  info->num_qo_heads = num_qo_heads;
   return KUNSERVE_OK;
 }
 
@@ -353,6 +470,8 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
                 pool->num_kv_heads);
   KSV_CHECK_ARG(info->tile_q == kTileQ, "plan tile %d does not match kernel tile %d",
                 info->tile_q, kTileQ);
+  KSV_CHECK_ARG(info->num_qo_heads == num_qo_heads, "plan made for %d q heads, called with %d",
+                info->num_qo_heads, num_qo_heads);
   if (info->num_tiles == 0) return KUNSERVE_OK;
   KSV_CHECK_ARG(plan_dev && q_indptr_dev && table->indptr_dev && table->indices_dev &&
                     table->kv_len_dev,
@@ -384,8 +503,8 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   a.tiles = plan_dev;
   a.ratio = num_qo_heads / pool->num_kv_heads;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
-  dim3 grid(info->num_tiles, num_qo_heads);
-  paged_prefill_kernel<<<grid, kThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
+  paged_prefill_kernel<<<dim3(info->num_tiles), kThreads, 0,
+                         reinterpret_cast<hipStream_t>(stream)>>>(a);
   KSV_CHECK_LAUNCH();
   return KUNSERVE_OK;
 }

@@ -201,21 +201,21 @@ class DecodePlan:
 
 
 class PrefillPlan:
-    """Query tiles of the prefill rows (kunserve_prefill_plan)."""
+    """(row, q tile, q head) work items of the prefill rows, XCD-ordered
+    (kunserve_prefill_plan)."""
 
     def __init__(self, q_indptr_host: Sequence[int], kv_len_host: Sequence[int],
-                 device: torch.device):
+                 num_qo_heads: int, num_kv_heads: int, device: torch.device):
         qi = _i32(q_indptr_host)
         kv = _i32(kv_len_host)
         n = len(kv)
         if len(qi) != n + 1:
             raise ValueError("q_indptr must have num_seqs + 1 entries")
-        q_lens = np.diff(qi)
-        cap = 2 * int(np.sum((q_lens + 127) // 128)) + 2
-        buf = np.zeros(cap, dtype=np.int32)
+        cap = int(_lib.lib().kunserve_prefill_plan_bound(qi.ctypes.data, n, num_qo_heads))
+        buf = np.zeros(max(cap, 3), dtype=np.int32)
         self.info = _lib.PrefillPlanInfo()
-        _lib.call("kunserve_prefill_plan", qi.ctypes.data if n else None,
-                  kv.ctypes.data if n else None, n, buf.ctypes.data, buf.size,
+        _lib.call("kunserve_prefill_plan", qi.ctypes.data, kv.ctypes.data if n else None, n,
+                  num_qo_heads, num_kv_heads, buf.ctypes.data, buf.size,
                   ctypes.byref(self.info))
         self.plan_host = buf[: self.info.plan_ints].copy()
         self.plan = torch.from_numpy(self.plan_host).to(device) if self.info.plan_ints else None
@@ -417,7 +417,7 @@ class AttentionStep:
                 tokens = torch.from_numpy(tok.astype(np.int64)).to(dev)
                 qi = np.zeros(pre_rows.size + 1, dtype=np.int32)
                 np.cumsum(q_lens[pre_rows], out=qi[1:])
-            plan = PrefillPlan(qi, self.kv_len[pre_rows], dev)
+            plan = PrefillPlan(qi, self.kv_len[pre_rows], num_qo_heads, pool.num_kv_heads, dev)
             self.prefill = _Subset(pre_rows, tokens, table, torch.from_numpy(qi).to(dev), plan)
 
     def run(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

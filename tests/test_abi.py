@@ -77,20 +77,44 @@ def test_decode_plan_rejects_bad_arguments():
     assert e.value.code == _lib.ENOSPC
 
 
-def test_prefill_plan_tiles():
+def _prefill_plan(q_indptr, kv, hq, hkv):
+    cap = _lib.lib().kunserve_prefill_plan_bound(q_indptr.ctypes.data, len(kv), hq)
+    buf = np.zeros(cap, dtype=np.int32)
+    info = _lib.PrefillPlanInfo()
+    _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, kv.ctypes.data, len(kv), hq, hkv,
+              buf.ctypes.data, cap, ctypes.byref(info))
+    return info, buf[:info.plan_ints].reshape(-1, 3)
+
+
+@pytest.mark.parametrize("hq,hkv,n", [(4, 4, 3), (8, 2, 3), (32, 32, 16), (1, 1, 1)])
+def test_prefill_plan_covers_every_tile_once(hq, hkv, n):
+    rng = np.random.default_rng(hq + n)
+    q_lens = rng.integers(0, 900, n)
+    q_indptr = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    kv = (q_lens + rng.integers(0, 3000, n)).astype(np.int32)
+    info, items = _prefill_plan(q_indptr, kv, hq, hkv)
+    tq = info.tile_q
+    assert info.num_tiles % 8 == 0 and info.num_tiles == len(items)
+    real = items[items[:, 0] >= 0]
+    want = {(b, q0, h) for b in range(n) for q0 in range(0, int(q_lens[b]), tq)
+            for h in range(hq)}
+    assert set(map(tuple, real.tolist())) == want and len(real) == len(want)
+    # items that read the same K/V (row, KV head) sit on one XCD unless split
+    xcd = {}
+    for L, (b, q0, h) in enumerate(items.tolist()):
+        if b >= 0:
+            xcd.setdefault((b, h // (hq // hkv)), set()).add(L % 8)
+    if len(xcd) >= 16:
+        assert all(len(v) == 1 for v in xcd.values())
+
+
+def test_prefill_plan_rejects_short_kv():
     q_indptr = np.array([0, 300, 301, 301 + 512], dtype=np.int32)
-    kv = np.array([1000, 1, 512], dtype=np.int32)
+    bad = np.array([5, 1, 512], dtype=np.int32)   # kv_len shorter than q_len
     buf = np.zeros(64, dtype=np.int32)
     info = _lib.PrefillPlanInfo()
-    _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, kv.ctypes.data, 3, buf.ctypes.data,
-              64, ctypes.byref(info))
-    tiles = buf[:info.plan_ints].reshape(-1, 2)
-    assert info.tile_q == 128
-    want = {(0, 0), (0, 128), (0, 256), (1, 0), (2, 0), (2, 128), (2, 256), (2, 384)}
-    assert set(map(tuple, tiles.tolist())) == want and len(tiles) == len(want)
-    bad = np.array([5, 1, 512], dtype=np.int32)   # kv_len shorter than q_len
     with pytest.raises(_lib.KunserveError):
-        _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, bad.ctypes.data, 3,
+        _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, bad.ctypes.data, 3, 4, 4,
                   buf.ctypes.data, 64, ctypes.byref(info))
 
 

@@ -45,7 +45,7 @@ def run_prefill(pool, layer, q_lens, kv, indptr, indices, q_indptr, hq, device, 
     T = int(q_indptr[-1])
     q = random_tensor((T, hq, pool.head_dim), device, seed)
     table = table_from_csr(indptr, indices, kv, device)
-    plan = PrefillPlan(q_indptr, kv, device)
+    plan = PrefillPlan(q_indptr, kv, hq, pool.num_kv_heads, device)
     out = paged_prefill(pool, layer, table, torch.from_numpy(q_indptr).to(device), q, plan)
     torch.cuda.synchronize()
     return q, out
@@ -103,7 +103,7 @@ def test_chunked_prefill_workload_sampled(device):
         qi = torch.from_numpy(q_indptr).to(device)
         append_kv(pool, 0, table, qi, k_new, v_new)
         q = random_tensor((T, w.num_qo_heads, w.head_dim), device, 300 + i)
-        out = paged_prefill(pool, 0, table, qi, q, PrefillPlan(q_indptr, kv, device))
+        out = paged_prefill(pool, 0, table, qi, q, PrefillPlan(q_indptr, kv, w.num_qo_heads, w.num_kv_heads, device))
         if i in checked:
             want = oracle_prefill(pool, 0, q, q_indptr, indptr, indices, kv)
             assert max_abs(out, want) <= ATOL
