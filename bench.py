@@ -8,10 +8,13 @@ over the 32 layers (one launch per layer, each layer with its own q).
 `value` is algorithmic KV bytes moved per second (K and V of every cached
 token once, plus q, out and page ids) with all inputs resident in HBM.
 
-Also measured (the `prefill` and `block_copy` objects): chunked-prefill
-attention with K/V append (16 sequences, prompts U[512, 4096], prefixes
-U[0, 2048], chunk 512) as MFMA utilisation of the fp16 dense peak, and the
-8192-block remap copy as HBM bandwidth.
+Also measured: `prefill` — chunked-prefill attention with K/V append (16
+sequences, prompts U[512, 4096], prefixes U[0, 2048], chunk 512) as MFMA
+utilisation of the fp16 dense peak; `gqa_decode` — Llama-3-8B GQA decode
+(32/8 heads, batch 128, contexts U[1024, 8192]) as HBM bandwidth; `remap` —
+the 8192-block remap copy as HBM bandwidth and a Llama-2-70B layer decode
+(64/8 heads, batch 256) on the remapped tables, bit-exact against the
+original tables.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
 """
@@ -68,34 +71,28 @@ class LaunchTimer:
 # ------------------------------------------------------------------ decode
 
 
-def bench_decode(args, device):
+def measure_decode(w, pool, layers, args, device, indices_override=None):
+    """Times paged_decode over `layers` of `pool` for workload `w`: one step
+    is one launch per layer. Returns the timing and the objects used."""
     import kunserve_amd as ks
-    from kunserve_amd import workloads
 
-    w = workloads.llama2_7b_decode()
-    log(f"decode workload: {w.name}; tokens {int(w.kv_len.sum())}, "
-        f"{w.kv_bytes_per_layer() / 2**30:.3f} GiB per layer")
     gen = torch.Generator(device=device)
-    gen.manual_seed(w.seed)
-    pool = ks.KVPool.allocate(w.num_pages, w.num_layers, w.num_kv_heads, w.page_size, w.head_dim,
-                              device)
-    fill_random_(pool.k, gen)
-    fill_random_(pool.v, gen)
+    gen.manual_seed(w.seed + 7)
     indptr, indices = w.csr()
+    if indices_override is not None:
+        indices = indices_override
     table = ks.PageTable(indptr, indices, w.kv_len, device)
     plan = ks.DecodePlan(w.kv_len, w.num_qo_heads, w.num_kv_heads, device,
                          part_tokens=args.part_tokens)
     ws = torch.zeros(max(plan.workspace_bytes(w.head_dim), 1), dtype=torch.uint8, device=device)
     qs = [torch.randn((w.batch, w.num_qo_heads, w.head_dim), generator=gen, device=device
-                      ).to(torch.float16) for _ in range(w.num_layers)]
+                      ).to(torch.float16) for _ in layers]
     out = torch.empty_like(qs[0])
-    log(f"plan: {plan.info.num_work} work items x {w.num_qo_heads // plan.info.group_size} "
-        f"head groups, part_tokens {plan.info.part_tokens}, {plan.info.num_merge} merged rows")
 
     def step(timer=None):
-        for layer in range(w.num_layers):
+        for i, layer in enumerate(layers):
             s = timer.start() if timer else None
-            ks.paged_decode(pool, layer, table, qs[layer], plan, out=out, workspace=ws)
+            ks.paged_decode(pool, layer, table, qs[i], plan, out=out, workspace=ws)
             if timer:
                 timer.stop(s)
 
@@ -113,27 +110,110 @@ def bench_decode(args, device):
     for _ in range(args.steps):
         step(timer)
     launch_ms = timer.mean_ms()
-
     bytes_per_layer = w.kv_bytes_per_layer()
-    bytes_per_step = bytes_per_layer * w.num_layers
-    gbs = bytes_per_step * args.steps / elapsed / 1e9
-    achieved = bytes_per_layer / (launch_ms * 1e-3) / 1e9
-    res = {
-        "value": gbs,
+    return {
+        "value": bytes_per_layer * len(layers) * args.steps / elapsed / 1e9,
         "ms_per_step": elapsed / args.steps * 1e3,
         "launch_ms": launch_ms,
-        "achieved": achieved,
+        "achieved": bytes_per_layer / (launch_ms * 1e-3) / 1e9,
         "bytes_per_layer": bytes_per_layer,
-        "workload": w,
-        "plan": plan,
-        "pool": pool,
-        "table": table,
-        "qs": qs,
+        "workload": w, "plan": plan, "pool": pool, "table": table, "qs": qs,
     }
-    log(f"decode: {res['ms_per_step']:.3f} ms/step, {gbs:.1f} GB/s whole-step; "
-        f"per launch {launch_ms * 1e3:.1f} us = {achieved:.1f} GB/s "
-        f"({achieved / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
+
+
+def bench_decode(args, device):
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+
+    w = workloads.llama2_7b_decode()
+    log(f"decode workload: {w.name}; tokens {int(w.kv_len.sum())}, "
+        f"{w.kv_bytes_per_layer() / 2**30:.3f} GiB per layer")
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    pool = ks.KVPool.allocate(w.num_pages, w.num_layers, w.num_kv_heads, w.page_size, w.head_dim,
+                              device)
+    fill_random_(pool.k, gen)
+    fill_random_(pool.v, gen)
+    res = measure_decode(w, pool, list(range(w.num_layers)), args, device)
+    plan = res["plan"]
+    log(f"plan: {plan.info.num_work} work items x {w.num_qo_heads // plan.info.group_size} "
+        f"head groups, part_tokens {plan.info.part_tokens}, {plan.info.num_merge} merged rows")
+    log(f"decode: {res['ms_per_step']:.3f} ms/step, {res['value']:.1f} GB/s whole-step; "
+        f"per launch {res['launch_ms'] * 1e3:.1f} us = {res['achieved']:.1f} GB/s "
+        f"({res['achieved'] / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
     return res
+
+
+def bench_gqa(args, device):
+    """Llama-3-8B GQA decode (32 Q / 8 KV heads, batch 128, contexts
+    U[1024, 8192]), one layer per launch."""
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+
+    w = workloads.llama3_8b_gqa_decode()
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    pool = ks.KVPool.allocate(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device)
+    fill_random_(pool.k, gen)
+    fill_random_(pool.v, gen)
+    res = measure_decode(w, pool, [0], args, device)
+    log(f"gqa decode: {w.name}: per launch {res['launch_ms'] * 1e3:.1f} us = "
+        f"{res['achieved']:.1f} GB/s ({res['achieved'] / HBM_PEAK_GBS * 100:.1f}% of HBM peak), "
+        f"part_tokens {res['plan'].info.part_tokens}, group {res['plan'].info.group_size}")
+    return {"workload": w.name, "launch_us": res["launch_ms"] * 1e3, "gbs": res["achieved"],
+            "hbm_frac": res["achieved"] / HBM_PEAK_GBS, "bytes_per_launch": res["bytes_per_layer"]}
+
+
+def bench_remap(args, device):
+    """Block remap under memory pressure: 8192 random 2 MiB blocks (32
+    layers x 8 heads x 16 x 128, K+V) copied between disjoint pool regions,
+    then a Llama-2-70B layer decode (64 Q / 8 KV heads, batch 256) on tables
+    that point at the copies; its output must equal, bit for bit, the
+    decode on the original tables."""
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+
+    r = workloads.kv_remap()
+    gen = torch.Generator(device=device)
+    gen.manual_seed(r.seed)
+    pool = ks.KVPool.allocate(r.num_pages, r.num_layers, r.num_kv_heads, r.page_size,
+                              r.head_dim, device)
+    fill_random_(pool.k, gen)
+    fill_random_(pool.v, gen)
+    src = torch.from_numpy(r.src).to(device)
+    dst = torch.from_numpy(r.dst).to(device)
+    reps = max(2, args.steps // 4)
+    ks.copy_blocks(pool, src, dst)
+    torch.cuda.synchronize()
+    timer = LaunchTimer()
+    for _ in range(reps):
+        s = timer.start()
+        ks.copy_blocks(pool, src, dst)
+        timer.stop(s)
+    copy_ms = timer.mean_ms()
+    copy_gbs = r.copy_bytes() / (copy_ms * 1e-3) / 1e9
+    log(f"block copy: {len(r.src)} blocks of {r.copy_bytes() / 4 / len(r.src) / 2**20:.0f} MiB "
+        f"(K and V), {copy_ms:.3f} ms = {copy_gbs:.1f} GB/s "
+        f"({copy_gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
+    w, w2 = r.decode, r.decode_remapped
+    dec = measure_decode(w2, pool, [0], args, device)
+    out_remapped = ks.paged_decode(pool, 0, dec["table"], dec["qs"][0], dec["plan"])
+    indptr, indices = w.csr()
+    table0 = ks.PageTable(indptr, indices, w.kv_len, device)
+    out_orig = ks.paged_decode(pool, 0, table0, dec["qs"][0], dec["plan"])
+    torch.cuda.synchronize()
+    same = bool(torch.equal(out_orig.view(torch.int16), out_remapped.view(torch.int16)))
+    log(f"70b decode on remapped tables: per launch {dec['launch_ms'] * 1e3:.1f} us = "
+        f"{dec['achieved']:.1f} GB/s ({dec['achieved'] / HBM_PEAK_GBS * 100:.1f}% of HBM peak); "
+        f"bit-exact vs original tables: {same}")
+    if not same:
+        print("remapped decode differs from the original tables", file=sys.stderr)
+        sys.exit(1)
+    return {"copy": {"workload": f"remap copy {len(r.src)} blocks x 2 MiB (K+V)",
+                     "ms": copy_ms, "gbs": copy_gbs, "hbm_frac": copy_gbs / HBM_PEAK_GBS},
+            "decode": {"workload": w.name, "launch_us": dec["launch_ms"] * 1e3,
+                       "gbs": dec["achieved"], "hbm_frac": dec["achieved"] / HBM_PEAK_GBS,
+                       "bit_exact_vs_original_tables": same}}
 
 
 def check_decode_sample(res, device) -> float:
@@ -251,37 +331,6 @@ def bench_prefill(args, device):
             "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS}
 
 
-# -------------------------------------------------------------- block copy
-
-
-def bench_copy(args, device):
-    import kunserve_amd as ks
-    from kunserve_amd import workloads
-
-    r = workloads.kv_remap()
-    n_pages = 2 * len(r.src)
-    pool = ks.KVPool.allocate(n_pages, r.num_layers, r.num_kv_heads, r.page_size, r.head_dim,
-                              device)
-    pool.k.fill_(1.0)
-    pool.v.fill_(2.0)
-    src = torch.from_numpy(r.src).to(device)
-    dst = torch.from_numpy(r.dst).to(device)
-    reps = max(2, args.steps // 4)
-    ks.copy_blocks(pool, src, dst)
-    torch.cuda.synchronize()
-    timer = LaunchTimer()
-    for _ in range(reps):
-        s = timer.start()
-        ks.copy_blocks(pool, src, dst)
-        timer.stop(s)
-    ms = timer.mean_ms()
-    gbs = r.copy_bytes() / (ms * 1e-3) / 1e9
-    log(f"block copy: {len(r.src)} blocks of {r.copy_bytes() / 4 / len(r.src) / 2**20:.0f} MiB "
-        f"(K and V), {ms:.3f} ms = {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
-    return {"workload": f"remap copy {len(r.src)} blocks x 2 MiB (K+V)", "ms": ms, "gbs": gbs,
-            "hbm_frac": gbs / HBM_PEAK_GBS}
-
-
 def load_traffic():
     path = os.path.join(PROFILE_DIR, "paged_decode_llama2_7b_traffic.json")
     if not os.path.exists(path):
@@ -296,7 +345,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
-    ap.add_argument("--only", choices=["decode", "prefill", "copy"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "gqa", "remap"], default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     args = ap.parse_args()
@@ -318,8 +367,11 @@ def main():
     if args.only == "prefill":
         print(json.dumps({"prefill": bench_prefill(args, device)}))
         return
-    if args.only == "copy":
-        print(json.dumps({"block_copy": bench_copy(args, device)}))
+    if args.only == "gqa":
+        print(json.dumps({"gqa_decode": bench_gqa(args, device)}))
+        return
+    if args.only == "remap":
+        print(json.dumps({"remap": bench_remap(args, device)}))
         return
 
     dec = bench_decode(args, device)
@@ -335,11 +387,13 @@ def main():
     w = dec["workload"]
     del dec["pool"], dec["qs"]
     torch.cuda.empty_cache()
-    prefill = copy = None
+    prefill = gqa = remap = None
     if args.only is None:
         prefill = bench_prefill(args, device)
         torch.cuda.empty_cache()
-        copy = bench_copy(args, device)
+        gqa = bench_gqa(args, device)
+        torch.cuda.empty_cache()
+        remap = bench_remap(args, device)
         torch.cuda.empty_cache()
 
     line = {
@@ -376,7 +430,8 @@ def main():
         },
         "cpu_baseline": cpu,
         "prefill": prefill,
-        "block_copy": copy,
+        "gqa_decode": gqa,
+        "remap": remap,
     }
     print(json.dumps(line))
 

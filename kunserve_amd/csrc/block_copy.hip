@@ -6,16 +6,21 @@
 // Copy and pack/scatter are HBM-bound: every byte is read once and written
 // once. One kernel serves all three: it walks "spans" (contiguous byte
 // ranges) addressed through an optional id list on each side, and each
-// workgroup streams a 32 KiB chunk of one span with 16-byte vector loads,
-// eight loads in flight per lane before the first store.
+// workgroup streams a chunk of one span with 16-byte vector loads, eight
+// loads in flight per lane before the first store.
 #include "common.hpp"
 
 namespace kunserve {
 namespace {
 
-constexpr int kCopyThreads = 256;
-constexpr int kCopyUnroll = 8;
-constexpr int64_t kCopyChunk = int64_t(kCopyThreads) * 16 * kCopyUnroll;  // 32 KiB
+// Two launch shapes: large spans (whole blocks of many layers) use
+// 1024-thread workgroups that each stream 256 KiB (two rounds of 8 x 16 B
+// per lane); slabs under 256 KiB use 256-thread workgroups on 32 KiB
+// chunks. Both keep eight 16-byte loads per lane in flight before storing.
+constexpr int kUnroll = 8;
+constexpr int kSmallThreads = 256, kSmallRounds = 1;
+constexpr int kLargeThreads = 1024, kLargeRounds = 2;
+constexpr int64_t chunk_bytes(int threads, int rounds) { return int64_t(threads) * 16 * kUnroll * rounds; }
 
 // One side of a copy: span s of item j lives at
 //   base + id(j) * pitch + s * span_stride      (bytes)
@@ -35,12 +40,14 @@ struct CopyJob {
   int64_t n;             // items
   int32_t spans;         // spans per item
   int64_t span_bytes;    // multiple of 16
-  int64_t chunks;        // ceil(span_bytes / kCopyChunk)
 };
 
 // Grid: x = item, y = chunk of the span, z = span. All index math is
-// scalar; each lane keeps 8 x 16 bytes in flight.
-__global__ __launch_bounds__(kCopyThreads) void span_copy_kernel(CopyJob job) {
+// scalar; loads and stores are non-temporal (each byte is touched once).
+template <int THREADS, int ROUNDS>
+__global__ __launch_bounds__(THREADS) void span_copy_kernel(CopyJob job) {
+  constexpr int64_t kChunk = chunk_bytes(THREADS, ROUNDS);
+  constexpr int32_t kRound = THREADS * 16 * kUnroll;
   const int64_t item = blockIdx.x;
   const int64_t chunk = blockIdx.y;
   const int64_t span = blockIdx.z;
@@ -49,39 +56,49 @@ __global__ __launch_bounds__(kCopyThreads) void span_copy_kernel(CopyJob job) {
   const int64_t did = job.dst.ids ? job.dst.ids[item] : item;
   if (sid < 0 || sid >= job.src.limit || did < 0 || did >= job.dst.limit) return;
 
-  const int64_t start = chunk * kCopyChunk;
+  const int64_t start = chunk * kChunk;
   const char* src = job.src.base + sid * job.src.pitch + span * job.src.span_stride + start;
   char* dst = job.dst.base + did * job.dst.pitch + span * job.dst.span_stride + start;
-  const int32_t avail = int32_t(min<int64_t>(job.span_bytes - start, kCopyChunk));
+  const int32_t avail = int32_t(min<int64_t>(job.span_bytes - start, kChunk));
   const int32_t lane_off = int32_t(threadIdx.x) * 16;
 
-  u32x4 buf[kCopyUnroll];
-  if (avail == kCopyChunk) {
+  if (avail == kChunk) {
+#pragma unroll 1
+    for (int r = 0; r < ROUNDS; ++r) {
+      u32x4 buf[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u)
-      buf[u] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(src + lane_off + u * kCopyThreads * 16));
+      for (int u = 0; u < kUnroll; ++u)
+        buf[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(src + r * kRound + lane_off + u * THREADS * 16));
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u)
-      __builtin_nontemporal_store(buf[u],
-                                  reinterpret_cast<u32x4*>(dst + lane_off + u * kCopyThreads * 16));
+      for (int u = 0; u < kUnroll; ++u)
+        __builtin_nontemporal_store(
+            buf[u], reinterpret_cast<u32x4*>(dst + r * kRound + lane_off + u * THREADS * 16));
+    }
   } else {
     // Last, partial chunk of a span.
-    for (int32_t off = lane_off; off < avail; off += kCopyThreads * 16)
+    for (int32_t off = lane_off; off < avail; off += THREADS * 16)
       *reinterpret_cast<u32x4*>(dst + off) = *reinterpret_cast<const u32x4*>(src + off);
   }
 }
 
 int launch_job(const CopyJob& job, hipStream_t stream) {
   if (job.n == 0 || job.spans == 0) return KUNSERVE_OK;
+  const bool large = job.span_bytes >= chunk_bytes(kLargeThreads, kLargeRounds);
+  const int64_t chunk = large ? chunk_bytes(kLargeThreads, kLargeRounds)
+                              : chunk_bytes(kSmallThreads, kSmallRounds);
+  const int64_t chunks = (job.span_bytes + chunk - 1) / chunk;
   KSV_CHECK_ARG(job.n < (int64_t(1) << 31), "copy of %lld items exceeds one launch",
                 (long long)job.n);
-  KSV_CHECK_ARG(job.chunks <= 65535 && job.spans <= 65535,
+  KSV_CHECK_ARG(chunks <= 65535 && job.spans <= 65535,
                 "span of %lld bytes x %d spans exceeds the launch geometry",
                 (long long)job.span_bytes, job.spans);
-  dim3 grid(static_cast<unsigned>(job.n), static_cast<unsigned>(job.chunks),
+  dim3 grid(static_cast<unsigned>(job.n), static_cast<unsigned>(chunks),
             static_cast<unsigned>(job.spans));
-  span_copy_kernel<<<grid, kCopyThreads, 0, stream>>>(job);
+  if (large)
+    span_copy_kernel<kLargeThreads, kLargeRounds><<<grid, kLargeThreads, 0, stream>>>(job);
+  else
+    span_copy_kernel<kSmallThreads, kSmallRounds><<<grid, kSmallThreads, 0, stream>>>(job);
   KSV_CHECK_LAUNCH();
   return KUNSERVE_OK;
 }
@@ -135,7 +152,6 @@ extern "C" int kunserve_copy_blocks(const kunserve_kv_pool* pool, const int32_t*
     job.spans = pool->num_layers;
     job.span_bytes = g.slab_bytes;
   }
-  job.chunks = (job.span_bytes + kCopyChunk - 1) / kCopyChunk;
   for (Side* s : {&job.src, &job.dst}) {
     s->pitch = pool->page_stride * 2;
     s->span_stride = pool->layer_stride * 2;
@@ -186,7 +202,6 @@ int pack_or_scatter(const kunserve_kv_pool* pool, int32_t layer_begin, int32_t l
     job.n = n;
     job.spans = nl;
     job.span_bytes = g.slab_bytes;
-    job.chunks = (job.span_bytes + kCopyChunk - 1) / kCopyChunk;
     Side pool_side{};
     pool_side.base = static_cast<char*>(kv ? pool->v : pool->k) +
                      int64_t(layer_begin) * pool->layer_stride * 2;
