@@ -332,11 +332,16 @@ def bench_prefill(args, device):
 
 
 def load_traffic():
-    path = os.path.join(PROFILE_DIR, "paged_decode_llama2_7b_traffic.json")
+    """HBM bytes per decode launch measured by rocprofv3 (FETCH_SIZE and
+    WRITE_SIZE passes, scaled by a known-size copy); None if not recorded."""
+    import re
+
+    path = os.path.join(PROFILE_DIR, "paged_decode_llama2_7b_traffic.md")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        m = re.search(r"^hbm_bytes_per_launch = (\d+)$", f.read(), re.M)
+    return int(m.group(1)) if m else None
 
 
 def main():
