@@ -242,6 +242,226 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
+// GQA decode on MFMA (head_dim 128, G = 8 query heads per KV head).
+// With G query heads sharing each K/V byte the VALU form above needs ~G
+// dot products and G x 8 FMAs per token row and lane, which caps it below
+// the HBM rate for G = 8. Here both contractions run on
+// v_mfma_f32_16x16x32_f16:
+//  * K and V are read exactly as in the VALU kernel (each load instruction
+//    covers 4 whole token rows, 1 KiB contiguous per wave: measured ~15%
+//    more bandwidth than reading MFMA operands straight from memory) and
+//    parked in a per-wave LDS block, row-major with the 16-byte chunk index
+//    XORed with (token & 15).
+//  * S^T[16 tokens x 16 heads] = K . Q^T, A operand = 16 K rows from LDS
+//    (ds_read_b128), B operand = Q^T (head lane%16, zero for lanes >= G).
+//  * O^T[16 dims x 16 heads] += V^T . P^T over 32 tokens: the A operand
+//    gathers 8 tokens of one dim from the V rows (16-bit LDS reads, no
+//    bank conflicts under the swizzle); P^T is the S^T accumulator itself
+//    packed to fp16: lane (head j, group tg) holds tokens 4tg..4tg+3 of
+//    each 16-token half, and the V gather uses the same token order.
+//  * Online softmax per head column in fp32 with a lazy running max, merged
+//    across waves through LDS; partial results as in the VALU kernel.
+template <int G>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void paged_decode_mfma_kernel(DecodeArgs a) {
+  constexpr int D = 128;
+  constexpr int STEP = 32;                  // tokens per wave iteration
+  constexpr int LOADS = STEP / 4;           // 16-byte loads per lane per step (K and V each)
+  constexpr int BLK = STEP * D;             // halves per per-wave K (or V) block
+  static_assert(G <= 16, "one 16-column MFMA tile of query heads");
+
+  __shared__ int s_pages[kMaxPartPages];
+  __shared__ __attribute__((aligned(16))) f16 s_kv[kWaves * BLK];   // 32 KiB: K, then V
+  __shared__ float s_m[kWaves][G];
+  __shared__ float s_l[kWaves][G];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int j = lane & 15;     // MFMA row / column index of this lane
+  const int tg = lane >> 4;    // MFMA k group / C row group
+  const int lrow = lane >> 4;  // load layout: token row within a 4-row load
+  const int lcol = lane & 15;  // load layout: 16-byte chunk of the row
+
+  const int32_t* w = a.work + 4 * blockIdx.x;
+  const int seq = w[0], tb = w[1], te = w[2], slot = w[3];
+  const int hq0 = blockIdx.y * G;
+  const int hkv = hq0 / a.ratio;
+  const int page_mask = (1 << a.page_shift) - 1;
+
+  const int pb = tb >> a.page_shift;
+  const int np = te > tb ? ((te - 1) >> a.page_shift) + 1 - pb : 0;
+  const int32_t* seq_pages = a.indices + a.indptr[seq];
+  for (int i = tid; i < np; i += kThreads) {
+    const int p = seq_pages[pb + i];
+    s_pages[i] = (p >= 0 && p < a.num_pages) ? p : -1;
+  }
+
+  // Q^T as the B operand: dim step s covers dims 32s + 8tg .. +8 of head j.
+  f16x8 qb[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    qb[s] = j < G ? load_f16x8(a.q + int64_t(seq) * a.q_tok + int64_t(hq0 + j) * a.q_head +
+                               32 * s + 8 * tg)
+                  : f16x8{};
+  f32x4 o[8];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) o[mt] = f32x4{};
+  float m = kNegBig;   // running max of head j, scaled log2 units (same in all tg)
+  float lsum = 0.f;    // this lane's share of head j's sum
+  __syncthreads();
+
+  const f16* kb = a.k + int64_t(hkv) * a.head_stride + lcol * 8;
+  const f16* vb = a.v + int64_t(hkv) * a.head_stride + lcol * 8;
+  const int nsteps = (te - tb + STEP - 1) / STEP;
+  f16* sk = s_kv + wave * BLK;   // holds the step's K rows, then its V rows
+  f16* sv = sk;
+  // Element (token t, dim d) of a block: t*128 + (((d >> 3) ^ (t & 15)) << 3) + (d & 7).
+  auto blk_off = [](int t, int chunk) { return t * D + ((chunk ^ (t & 15)) << 3); };
+
+  struct Step {
+    f16x8 k[LOADS], v[LOADS];
+  };
+  auto load_step = [&](int c, Step& st) {
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int t = tb + c * STEP + 4 * i + lrow;
+      const int p = (c < nsteps && t < te) ? s_pages[(t >> a.page_shift) - pb] : -1;
+      const int64_t off = int64_t(p) * a.page_stride + int64_t(t & page_mask) * a.token_stride;
+      if (p >= 0) {
+        st.k[i] = load_f16x8_nt(kb + off);
+        st.v[i] = load_f16x8_nt(vb + off);
+      } else {
+        st.k[i] = f16x8{};
+        st.v[i] = f16x8{};
+      }
+    }
+  };
+  auto stash = [&](const f16x8 (&rows)[LOADS]) {
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i)
+      *reinterpret_cast<f16x8*>(&sk[blk_off(4 * i + lrow, lcol)]) = rows[i];
+  };
+  // Scores of the step whose K rows are in the block.
+  auto scores = [&](f32x4 (&sc)[2]) {
+    // LDS runs a wave's accesses in order; keep the compiler from moving them.
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int t = 16 * sub + j;
+      sc[sub] = f32x4{};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const f16x8 ka = *reinterpret_cast<const f16x8*>(&sk[blk_off(t, 4 * s + tg)]);
+        sc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sc[sub], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+  // Softmax of the scores and O^T += V^T . P^T with the V rows in the block.
+  auto accumulate = [&](f32x4 (&sc)[2], int c) {
+    // Mask tokens past the partition; lane holds tokens 16 sub + 4 tg + v.
+    const int t0 = tb + c * STEP;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (t0 + 16 * sub + 4 * tg + v >= te) sc[sub][v] = -INFINITY;
+        mx = fmaxf(mx, sc[sub][v]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
+    if (__any(mx > m + 8.f)) {
+      const float m_new = mx > m + 8.f ? mx : m;
+      const float alpha = fast_exp2(m - m_new);
+      m = m_new;
+      lsum *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) o[mt] *= alpha;
+    }
+    f16x8 pb;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float p = fast_exp2(fmaf(sc[sub][v], a.scale_log2, -m));
+        lsum += p;
+        pb[sub * 4 + v] = f16(p);
+      }
+    __builtin_amdgcn_wave_barrier();
+    // O^T: A operand = V[token 16 sub + 4 tg + v][dim 16 mt + j] for e = 4 sub + v.
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const int d = 16 * mt + j;
+      f16x8 va;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = 16 * (e >> 2) + 4 * tg + (e & 3);
+        va[e] = sv[blk_off(t, d >> 3) + (d & 7)];
+      }
+      o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[mt], 0, 0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  // One register buffer: the next step's loads are issued once the current
+  // step's K and V rows are parked in LDS, and land during its math.
+  if (wave < nsteps) {
+    Step st;
+    int c = wave;
+    load_step(c, st);
+    while (c < nsteps) {
+      f32x4 sc[2];
+      stash(st.k);
+      scores(sc);
+      stash(st.v);   // overwrites the K rows: the score reads were issued first
+      load_step(c + kWaves, st);
+      accumulate(sc, c);
+      c += kWaves;
+    }
+  }
+
+  // Head j's sum over the 4 row groups of this wave.
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  __syncthreads();   // every wave is done with its K/V blocks: reuse them for the merge
+  float* s_o = reinterpret_cast<float*>(s_kv);   // [kWaves][G][D]
+  if (j < G) {
+    if (tg == 0) {
+      s_m[wave][j] = m;
+      s_l[wave][j] = lsum;
+    }
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) s_o[(wave * G + j) * D + 16 * mt + 4 * tg + v] = o[mt][v];
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    float mxw = kNegBig;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) mxw = fmaxf(mxw, s_m[wv][g]);
+    float ls = 0.f, acc = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) {
+      const float f = fast_exp2(s_m[wv][g] - mxw);
+      ls += s_l[wv][g] * f;
+      acc += s_o[(wv * G + g) * D + d] * f;
+    }
+    const float r = ls > 0.f ? acc / ls : 0.f;
+    const int hq = hq0 + g;
+    if (slot < 0) {
+      a.out[int64_t(seq) * a.o_tok + int64_t(hq) * a.o_head + d] = f16(r);
+    } else {
+      a.part_o[(int64_t(slot) * a.num_qo_heads + hq) * D + d] = r;
+      if (d == 0)
+        a.part_lse[int64_t(slot) * a.num_qo_heads + hq] = ls > 0.f ? mxw + __log2f(ls) : -INFINITY;
+    }
+  }
+}
+
 // Combines the partitions of split sequences: one wave per (sequence,
 // q head). Lane j first reads the log-sum-exp of partition j, so the
 // weights come from one round of loads; each lane then accumulates D/64
@@ -298,6 +518,16 @@ int pick_group(int ratio) {
 
 template <int D>
 int launch_decode(const DecodeArgs& a, int group, dim3 grid, hipStream_t s) {
+  if constexpr (D == 128) {
+    if (group == 4 || group == 8) {
+      if (group == 4)
+        paged_decode_mfma_kernel<4><<<grid, kThreads, 0, s>>>(a);
+      else
+        paged_decode_mfma_kernel<8><<<grid, kThreads, 0, s>>>(a);
+      KSV_CHECK_LAUNCH();
+      return KUNSERVE_OK;
+    }
+  }
   switch (group) {
     case 1: paged_decode_kernel<D, 1><<<grid, kThreads, 0, s>>>(a); break;
     case 2: paged_decode_kernel<D, 2><<<grid, kThreads, 0, s>>>(a); break;
