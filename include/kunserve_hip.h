@@ -201,6 +201,7 @@ typedef struct {
   int32_t tile_q;        /* q rows per tile                                */
   int32_t plan_ints;     /* int32 entries of the plan buffer in use       */
   int32_t num_qo_heads;  /* heads the plan was made for                    */
+  int32_t max_kv_len;    /* longest kv_len among the planned rows          */
 } kunserve_prefill_plan_info;
 
 /* Upper bound of the prefill plan length (int32 entries). */

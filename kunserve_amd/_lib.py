@@ -52,7 +52,7 @@ class DecodePlanInfo(Structure):
 
 class PrefillPlanInfo(Structure):
     _fields_ = [("num_tiles", c_int32), ("tile_q", c_int32), ("plan_ints", c_int32),
-                ("num_qo_heads", c_int32)]
+                ("num_qo_heads", c_int32), ("max_kv_len", c_int32)]
 
 
 # name -> (restype, argtypes); must match include/kunserve_hip.h.

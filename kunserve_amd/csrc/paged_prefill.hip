@@ -57,25 +57,40 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-// LDS layouts (element offsets within one buffer of kTileKV x kD halves;
-// the two buffers differ in bit 13, so buffer selection is an XOR too).
-// K: [token][dim], the 16-byte chunk index XORed with (token & 15).
-//    offset(t, chunk) = (t*128 | (t & 15) << 3) ^ (chunk << 3)
-__device__ __forceinline__ int sk_off(int t, int chunk) { return (t * kD | (t & 15) << 3) ^ (chunk << 3); }
-// V^T: [dim][token], tokens of each row stored in MFMA k-slot order: chunk
-// c = 2ks + h (8 halves) holds tokens 16ks + 4h + {0..3} and 16ks + 8 + 4h
-// + {0..3}, so one ds_read_b128 is one A operand. Chunk index XORed with
-// f(d) = (d ^ d >> 3) & 7.
-//    offset(d, c) = (d*64 | f(d) << 3) ^ (c << 3)
-__device__ __forceinline__ int vt_base(int d) { return d * kTileKV | ((d ^ (d >> 3)) & 7) << 3; }
-__device__ __forceinline__ int vt_tok(int t) {   // (chunk << 3) | position of token t
-  return ((2 * (t >> 4) + ((t >> 2) & 1)) << 3) | (((t >> 3) & 1) << 2) | (t & 3);
-}
-constexpr int kBufHalves = kTileKV * kD;   // 8192: bit 13
+// LDS layouts. Both tiles are row-major [token][dim] with padded rows, so
+// every operand address is a per-lane base plus an immediate offset:
+// K rows are 68 dwords apart: a column read by 8 lanes (8 rows, one 16-byte
+//    chunk) touches 8 distinct 4-bank groups.
+// V rows are 72 dwords apart: the transposing reads below fetch 32 bytes of 4
+//    consecutive rows per 16 lanes, which then start 8 banks apart.
+constexpr int kKPitch = kD + 8;     // halves
+constexpr int kVPitch = kD + 16;    // halves
+constexpr int kKHalves = kTileKV * kKPitch;
+constexpr int kVHalves = kTileKV * kVPitch;
 
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane group, lane i receives
+// element (i % 4) of the 8 bytes addressed by lanes 4k + i/4, k = 0..3. With
+// lanes 4k..4k+3 addressing 4 consecutive dims of token t_k, lane i gets
+// V[t_k][dbase + i] for k = 0..3: four tokens of its own dim.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f16x4 lds_read_tr16(const f16* p) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(f16x4, r);
+}
+
+// Page ids a workgroup stages in LDS (rows up to 32768 tokens at page 16).
+constexpr int kMaxStagedPages = 2048;
+
+// STAGED: the row's page ids are copied to LDS once, so the tile gathers
+// issue only K/V loads; waiting for an older tile's data then leaves the
+// newer tile's loads in flight. Rows with more pages than fit use the
+// global-lookup variant (same results).
+template <bool STAGED>
 __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) f16 sK[2 * kBufHalves];
-  __shared__ __attribute__((aligned(16))) f16 sV[2 * kBufHalves];
+  __shared__ int s_pg[STAGED ? kMaxStagedPages : 1];
+  __shared__ __attribute__((aligned(16))) f16 sK[2 * kKHalves];
+  __shared__ __attribute__((aligned(16))) f16 sV[2 * kVHalves];
 
   const int32_t* item = a.tiles + 3 * blockIdx.x;
   const int seq = item[0];
@@ -105,6 +120,14 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   const int wave_last_pos = prefix + min(q0 + wave * 32 + 31, q_len - 1);
   const int kv_end = prefix + min(q0 + kTileQ, q_len);   // exclusive
   const int ntiles = (kv_end + kTileKV - 1) / kTileKV;
+  if constexpr (STAGED) {
+    const int npg = kv_end > 0 ? ((kv_end - 1) >> a.page_shift) + 1 : 0;
+    for (int i = threadIdx.x; i < npg; i += kThreads) {
+      const int p = pages[i];
+      s_pg[i] = (p >= 0 && p < a.num_pages) ? p : -1;
+    }
+    __syncthreads();
+  }
 
   // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
   f16x8 qf[8];
@@ -123,56 +146,67 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   const f16* kbase = a.k + int64_t(hkv) * a.head_stride;
   const f16* vbase = a.v + int64_t(hkv) * a.head_stride;
 
-  f16x8 kr[kLoadsPerThread], vr[kLoadsPerThread];
-  auto fetch = [&](int n0) {
+  // Tile registers: two sets, so that the gather of tile n + 2 is in flight
+  // while tile n is computed and tile n + 1 waits to be parked in LDS. One
+  // tile's loads take about one HBM round trip, longer than a tile's math.
+  struct Regs {
+    f16x8 k[kLoadsPerThread], v[kLoadsPerThread];
+  };
+  auto fetch = [&](int n0, Regs& rg) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
       const int c = tid + kThreads * i;
       const int t = c >> 4, dc = c & 15;
       const int tok = n0 + t;
-      const int p = tok < kvl ? pages[tok >> a.page_shift] : -1;
-      if (p >= 0 && p < a.num_pages) {
-        const int64_t off =
-            int64_t(p) * a.page_stride + int64_t(tok & page_mask) * a.token_stride + dc * 8;
-        kr[i] = load_f16x8(kbase + off);
-        vr[i] = load_f16x8(vbase + off);
-      } else {
-        kr[i] = f16x8{};
-        vr[i] = f16x8{};
-      }
+      int p;
+      if constexpr (STAGED)
+        p = tok < kv_end ? s_pg[tok >> a.page_shift] : -1;
+      else
+        p = tok < kvl ? pages[tok >> a.page_shift] : -1;
+      // Unconditional loads (past-the-end tokens and bad ids read page 0,
+      // slot 0 and are zeroed), so the compiler can wait for the older
+      // register set while the newer one is in flight.
+      const bool ok = p >= 0 && p < a.num_pages;
+      const int64_t off =
+          (ok ? int64_t(p) * a.page_stride + int64_t(tok & page_mask) * a.token_stride : 0) +
+          dc * 8;
+      const f16x8 kx = load_f16x8(kbase + off);
+      const f16x8 vx = load_f16x8(vbase + off);
+      rg.k[i] = ok ? kx : f16x8{};
+      rg.v[i] = ok ? vx : f16x8{};
     }
   };
-  auto stash = [&](int buf) {
-    const int bo = buf * kBufHalves;
+  auto stash = [&](int buf, const Regs& rg) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
       const int c = tid + kThreads * i;
       const int t = c >> 4, dc = c & 15;
-      *reinterpret_cast<f16x8*>(&sK[bo ^ sk_off(t, dc)]) = kr[i];
-      const int tv = vt_tok(t);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sV[bo ^ vt_base(dc * 8 + j) ^ tv] = vr[i][j];
+      *reinterpret_cast<f16x8*>(&sK[buf * kKHalves + t * kKPitch + dc * 8]) = rg.k[i];
+      *reinterpret_cast<f16x8*>(&sV[buf * kVHalves + t * kVPitch + dc * 8]) = rg.v[i];
     }
   };
 
-  // Per-lane LDS bases (buffer 0); every operand address is one XOR away.
-  const int kb0 = sk_off(r, h);            // K rows r (mt = 0) and r + 32 (^ 4096)
-  int vb[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) vb[dt] = vt_base(32 * dt + r) ^ (h << 3);
+  // Per-lane LDS bases; each operand read adds a compile-time offset.
+  // K A operand (S^T = K.Q^T): row 32 mt + r, dims 16 s + 8 h .. +8.
+  const int kb0 = r * kKPitch + 8 * h;
+  // V^T A operand via the transposing read: this lane supplies the address
+  // of token 4 (g / 2) + (i / 4) (+ 16 ks + 8 half), dims 16 (g % 2) + 4 (i % 4)
+  // (+ 32 dt), where g = lane / 16 and i = lane % 16.
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int vb0 = (4 * (g16 >> 1) + (i16 >> 2)) * kVPitch + 16 * (g16 & 1) + 4 * (i16 & 3);
 
   auto compute = [&](int buf, int n0) {
-    const int bo = buf * kBufHalves;
+    const f16* kt = sK + buf * kKHalves + kb0;
+    const f16* vt = sV + buf * kVHalves + vb0;
     // S^T tiles: rows = kv tokens 32*mt + i, columns = query rows.
     f32x16 st[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      const int kb = bo ^ kb0 ^ (mt << 12);
       st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-          *reinterpret_cast<const f16x8*>(&sK[kb]), qf[0], f32x16{}, 0, 0, 0);
+          *reinterpret_cast<const f16x8*>(kt + 32 * mt * kKPitch), qf[0], f32x16{}, 0, 0, 0);
 #pragma unroll
       for (int s = 1; s < 8; ++s) {
-        const f16x8 ka = *reinterpret_cast<const f16x8*>(&sK[kb ^ (s << 4)]);
+        const f16x8 ka = *reinterpret_cast<const f16x8*>(kt + 32 * mt * kKPitch + 16 * s);
         st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[s], st[mt], 0, 0, 0);
       }
     }
@@ -220,28 +254,46 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
       }
     lsum += ps;
 
-    // O^T[dims, rows] += V^T[dims, tokens] . P^T[tokens, rows]
+    // O^T[dims, rows] += V^T[dims, tokens] . P^T[tokens, rows]; the A operand
+    // for k-step ks is tokens 16ks + 4h + {0..3} then 16ks + 8 + 4h + {0..3}.
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const f16x8 va = *reinterpret_cast<const f16x8*>(&sV[bo ^ vb[dt] ^ (ks << 4)]);
+        const f16x4 lo = lds_read_tr16(vt + 16 * ks * kVPitch + 32 * dt);
+        const f16x4 hi = lds_read_tr16(vt + (16 * ks + 8) * kVPitch + 32 * dt);
+        const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[ks], o[dt], 0, 0, 0);
       }
     }
   };
 
-  fetch(0);
-  stash(0);
+  // Tile it is computed from LDS buffer it % 2 while tile it + 1 sits in
+  // registers (loads issued one iteration earlier) and tile it + 2 is being
+  // fetched into the other register set.
+  Regs ra, rb;
+  fetch(0, ra);
+  fetch(kTileKV, rb);
+  stash(0, ra);
   __syncthreads();
-  for (int it = 0; it < ntiles; ++it) {
-    const int n0 = it * kTileKV;
-    const int buf = it & 1;
-    const bool more = it + 1 < ntiles;
-    if (more) fetch(n0 + kTileKV);   // in flight during this tile's math
-    if (wave_active && n0 <= wave_last_pos) compute(buf, n0);
-    if (more) stash(buf ^ 1);        // that buffer was last read before the previous barrier
-    __syncthreads();
+  for (int it = 0; it < ntiles; it += 2) {
+    // even tile: next tile in rb, fetch it + 2 into ra
+    {
+      const int n0 = it * kTileKV;
+      fetch(n0 + 2 * kTileKV, ra);   // past the end: cache-resident dummy reads
+      if (wave_active && n0 <= wave_last_pos) compute(0, n0);
+      if (it + 1 < ntiles) stash(1, rb);   // buffer 1 was last read before the previous barrier
+      __syncthreads();
+    }
+    if (it + 1 >= ntiles) break;
+    // odd tile: next tile in ra, fetch it + 3 into rb
+    {
+      const int n0 = (it + 1) * kTileKV;
+      fetch(n0 + 2 * kTileKV, rb);
+      if (wave_active && n0 <= wave_last_pos) compute(1, n0);
+      if (it + 2 < ntiles) stash(0, ra);
+      __syncthreads();
+    }
   }
 
   lsum += __shfl_xor(lsum, 32);
@@ -445,6 +497,12 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
   info->tile_q = kTileQ;
   info->plan_ints = int32_t(need);
   info->num_qo_heads = num_qo_heads;
+  int32_t max_kv = 0;
+  for (int32_t b = 0; b < num_seqs; ++b) {
+    const int32_t ql = q_indptr_host[b + 1] - q_indptr_host[b];
+    if (ql > 0) max_kv = std::max(max_kv, kv_len_host[b]);
+  }
+  info->max_kv_len = max_kv;
   return KUNSERVE_OK;
 }
 
@@ -503,8 +561,13 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   a.tiles = plan_dev;
   a.ratio = num_qo_heads / pool->num_kv_heads;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
-  paged_prefill_kernel<<<dim3(info->num_tiles), kThreads, 0,
-                         reinterpret_cast<hipStream_t>(stream)>>>(a);
+  const int64_t pages_needed = (int64_t(info->max_kv_len) + pool->page_size - 1) / pool->page_size;
+  if (pages_needed <= kMaxStagedPages)
+    paged_prefill_kernel<true><<<dim3(info->num_tiles), kThreads, 0,
+                                 reinterpret_cast<hipStream_t>(stream)>>>(a);
+  else
+    paged_prefill_kernel<false><<<dim3(info->num_tiles), kThreads, 0,
+                                  reinterpret_cast<hipStream_t>(stream)>>>(a);
   KSV_CHECK_LAUNCH();
   return KUNSERVE_OK;
 }
