@@ -45,7 +45,8 @@ struct PrefillArgs {
   int64_t o_tok, o_head;
   const f16* k;   // pool K at the layer
   const f16* v;
-  int64_t page_stride, head_stride, token_stride;
+  int64_t head_stride;
+  uint32_t page_stride, token_stride;   // checked on the host to fit 32 bits
   int32_t num_pages;
   int32_t page_shift;
   const int32_t* indptr;
@@ -81,6 +82,10 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const f16* p) {
 
 // Page ids a workgroup stages in LDS (rows up to 32768 tokens at page 16).
 constexpr int kMaxStagedPages = 2048;
+
+// Source of the gathers of tokens past a row's end and of out-of-range page
+// ids: one zero K/V row, so staged tiles need no masking.
+__device__ __attribute__((aligned(16))) f16 g_zero_row[kD];
 
 // STAGED: the row's page ids are copied to LDS once, so the tile gathers
 // issue only K/V loads; waiting for an older tile's data then leaves the
@@ -149,40 +154,47 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   // Tile registers: two sets, so that the gather of tile n + 2 is in flight
   // while tile n is computed and tile n + 1 waits to be parked in LDS. One
   // tile's loads take about one HBM round trip, longer than a tile's math.
+  // Thread tid moves dims 8 (tid % 16) .. +8 of tokens tid / 16 + 32 i.
+  // The page ids of a gather are read one iteration ahead (pid), so no
+  // lookup latency sits in front of the loads.
+  const int ld_t = tid >> 4;
+  const int ld_c = (tid & 15) * 8;
   struct Regs {
     f16x8 k[kLoadsPerThread], v[kLoadsPerThread];
+  };
+  int pid[kLoadsPerThread];
+  auto read_ids = [&](int n0) {
+#pragma unroll
+    for (int i = 0; i < kLoadsPerThread; ++i) {
+      const int tok = n0 + ld_t + 32 * i;
+      int p = -1;
+      if constexpr (STAGED) {
+        if (tok < kv_end) p = s_pg[tok >> a.page_shift];
+      } else {
+        if (tok < kv_end) p = pages[tok >> a.page_shift];
+        p = (p >= 0 && p < a.num_pages) ? p : -1;
+      }
+      pid[i] = p;
+    }
   };
   auto fetch = [&](int n0, Regs& rg) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
-      const int c = tid + kThreads * i;
-      const int t = c >> 4, dc = c & 15;
-      const int tok = n0 + t;
-      int p;
-      if constexpr (STAGED)
-        p = tok < kv_end ? s_pg[tok >> a.page_shift] : -1;
-      else
-        p = tok < kvl ? pages[tok >> a.page_shift] : -1;
-      // Unconditional loads (past-the-end tokens and bad ids read page 0,
-      // slot 0 and are zeroed), so the compiler can wait for the older
-      // register set while the newer one is in flight.
-      const bool ok = p >= 0 && p < a.num_pages;
-      const int64_t off =
-          (ok ? int64_t(p) * a.page_stride + int64_t(tok & page_mask) * a.token_stride : 0) +
-          dc * 8;
-      const f16x8 kx = load_f16x8(kbase + off);
-      const f16x8 vx = load_f16x8(vbase + off);
-      rg.k[i] = ok ? kx : f16x8{};
-      rg.v[i] = ok ? vx : f16x8{};
+      const int tok = n0 + ld_t + 32 * i;
+      const uint64_t off = uint64_t(uint32_t(pid[i])) * a.page_stride +
+                           (uint32_t(tok & page_mask) * a.token_stride + ld_c);
+      // Past-the-end tokens and bad ids read the zero row (cache-resident).
+      const bool ok = pid[i] >= 0;
+      rg.k[i] = load_f16x8(ok ? kbase + off : g_zero_row + ld_c);
+      rg.v[i] = load_f16x8(ok ? vbase + off : g_zero_row + ld_c);
     }
   };
   auto stash = [&](int buf, const Regs& rg) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
-      const int c = tid + kThreads * i;
-      const int t = c >> 4, dc = c & 15;
-      *reinterpret_cast<f16x8*>(&sK[buf * kKHalves + t * kKPitch + dc * 8]) = rg.k[i];
-      *reinterpret_cast<f16x8*>(&sV[buf * kVHalves + t * kVPitch + dc * 8]) = rg.v[i];
+      const int t = ld_t + 32 * i;
+      *reinterpret_cast<f16x8*>(&sK[buf * kKHalves + t * kKPitch + ld_c]) = rg.k[i];
+      *reinterpret_cast<f16x8*>(&sV[buf * kVHalves + t * kVPitch + ld_c]) = rg.v[i];
     }
   };
 
@@ -272,17 +284,21 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   // registers (loads issued one iteration earlier) and tile it + 2 is being
   // fetched into the other register set.
   Regs ra, rb;
+  read_ids(0);
   fetch(0, ra);
+  read_ids(kTileKV);
   fetch(kTileKV, rb);
   stash(0, ra);
+  read_ids(2 * kTileKV);
   __syncthreads();
   for (int it = 0; it < ntiles; it += 2) {
     // even tile: next tile in rb, fetch it + 2 into ra
     {
       const int n0 = it * kTileKV;
-      fetch(n0 + 2 * kTileKV, ra);   // past the end: cache-resident dummy reads
+      fetch(n0 + 2 * kTileKV, ra);   // past the end: zero-row reads
       if (wave_active && n0 <= wave_last_pos) compute(0, n0);
       if (it + 1 < ntiles) stash(1, rb);   // buffer 1 was last read before the previous barrier
+      read_ids(n0 + 3 * kTileKV);
       __syncthreads();
     }
     if (it + 1 >= ntiles) break;
@@ -292,6 +308,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
       fetch(n0 + 2 * kTileKV, rb);
       if (wave_active && n0 <= wave_last_pos) compute(1, n0);
       if (it + 2 < ntiles) stash(0, ra);
+      read_ids(n0 + 3 * kTileKV);
       __syncthreads();
     }
   }
@@ -549,9 +566,16 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   a.o_head = out->head_stride;
   a.k = static_cast<const f16*>(pool->k) + int64_t(layer) * pool->layer_stride;
   a.v = static_cast<const f16*>(pool->v) + int64_t(layer) * pool->layer_stride;
-  a.page_stride = pool->page_stride;
+  // Gathers address a page with one 32 x 32 -> 64-bit multiply-add.
+  if (pool->page_stride > int64_t(UINT32_MAX) ||
+      int64_t(pool->page_size) * pool->token_stride > int64_t(UINT32_MAX)) {
+    set_error("prefill needs page_stride (%lld) and page_size x token_stride below 2^32",
+              (long long)pool->page_stride);
+    return KUNSERVE_EUNSUPPORTED;
+  }
+  a.page_stride = uint32_t(pool->page_stride);
   a.head_stride = pool->head_stride;
-  a.token_stride = pool->token_stride;
+  a.token_stride = uint32_t(pool->token_stride);
   a.num_pages = int32_t(pool->num_pages);
   a.page_shift = __builtin_ctz(pool->page_size);
   a.indptr = table->indptr_dev;
