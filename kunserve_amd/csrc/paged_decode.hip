@@ -36,6 +36,10 @@ constexpr int kMaxPartPages = kMaxPartTokens / kMinPageSize + 2;
 constexpr int kMinPartTokens = 256;
 constexpr float kNegBig = -1.0e30f;      // finite "minus infinity" for running maxima
 
+// Source of the loads of lanes past a partition's end and of bad page ids:
+// one zero K/V row (head_dim <= 256), so loaded data is never masked.
+__device__ __attribute__((aligned(16))) f16 g_zero_row[256];
+
 struct DecodeArgs {
   const f16* q;
   int64_t q_tok, q_head;
@@ -114,9 +118,9 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
     f16x8 k[kLoadsPerChunk], v[kLoadsPerChunk];
     bool ok[kLoadsPerChunk];
   };
-  // Loads are issued unconditionally (lanes past the partition read page 0,
-  // slot 0 of the head, a cache-resident line, and are zeroed afterwards):
-  // with no branch around them the compiler can wait for the current chunk
+  // Loads are issued unconditionally (lanes past the partition read the
+  // cache-resident zero row): with no branch around them and no use of the
+  // data until it is consumed, the compiler waits for the current chunk
   // while the next chunk's loads stay in flight.
   auto load_chunk = [&](int c, Chunk& ch) {
     const int t0 = tb + c * CHUNK;
@@ -126,12 +130,9 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
       const int pi = min((t >> a.page_shift) - pb, kMaxPartPages - 1);
       const int p = (c < nchunks && t < te) ? s_pages[pi] : -1;
       ch.ok[i] = p >= 0;
-      const int64_t off =
-          ch.ok[i] ? int64_t(p) * a.page_stride + int64_t(t & page_mask) * a.token_stride : 0;
-      const f16x8 kx = load_f16x8_nt(kb + off);
-      const f16x8 vx = load_f16x8_nt(vb + off);
-      ch.k[i] = ch.ok[i] ? kx : f16x8{};
-      ch.v[i] = ch.ok[i] ? vx : f16x8{};
+      const int64_t off = int64_t(max(p, 0)) * a.page_stride + int64_t(t & page_mask) * a.token_stride;
+      ch.k[i] = load_f16x8_nt(ch.ok[i] ? kb + off : g_zero_row + col * 8);
+      ch.v[i] = load_f16x8_nt(ch.ok[i] ? vb + off : g_zero_row + col * 8);
     }
   };
   auto consume = [&](const Chunk& ch) {
@@ -325,8 +326,8 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   struct Step {
     f16x8 k[LOADS], v[LOADS];
   };
-  // Unconditional loads (see the VALU kernel): past-the-end lanes read page
-  // 0, slot 0 of the head and are zeroed.
+  // Unconditional loads (see the VALU kernel): past-the-end lanes and bad
+  // page ids read the zero row.
   auto load_step = [&](int c, Step& st) {
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
@@ -334,12 +335,9 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
       const int pi = min((t >> a.page_shift) - pb, kMaxPartPages - 1);
       const int p = (c < nsteps && t < te) ? s_pages[pi] : -1;
       const bool ok = p >= 0;
-      const int64_t off =
-          ok ? int64_t(p) * a.page_stride + int64_t(t & page_mask) * a.token_stride : 0;
-      const f16x8 kx = load_f16x8_nt(kb + off);
-      const f16x8 vx = load_f16x8_nt(vb + off);
-      st.k[i] = ok ? kx : f16x8{};
-      st.v[i] = ok ? vx : f16x8{};
+      const int64_t off = int64_t(max(p, 0)) * a.page_stride + int64_t(t & page_mask) * a.token_stride;
+      st.k[i] = load_f16x8_nt(ok ? kb + off : g_zero_row + lcol * 8);
+      st.v[i] = load_f16x8_nt(ok ? vb + off : g_zero_row + lcol * 8);
     }
   };
   auto stash = [&](const f16x8 (&rows)[LOADS]) {
