@@ -7,14 +7,13 @@
 // Attention: flash-attention style on fp16 MFMA (v_mfma_f32_32x32x16_f16,
 // gfx950), fp32 accumulation and online softmax.
 //  * Workgroup = 8 waves = 256 query rows of one (sequence, q head); each
-//    wave owns 32 rows. Two waves share a SIMD, so one wave's softmax
-//    (VALU, exp) overlaps the other's MFMAs.
+//    wave owns 32 rows. Two waves share a SIMD (waves w and w + 4).
 //  * K/V tiles of 64 tokens are gathered from pages into double-buffered
-//    LDS (K row-major, V transposed), both with XOR swizzles so that the
-//    MFMA operand reads (ds_read_b128 for K, ds_read_b64 for V^T) and the
-//    staging writes are free of bank conflicts. The next tile's global
-//    loads are issued before the current tile's math, so their latency
-//    hides behind it; one barrier per tile.
+//    LDS, both row-major with padded rows. K operands are ds_read_b128 rows;
+//    V^T operands come from the gfx950 transposing read (ds_read_b64_tr_b16).
+//    The gather of the tile after next is issued before the current tile's
+//    math (two register sets), with its page ids read from LDS one
+//    iteration earlier; one barrier per tile.
 //  * S^T = K.Q^T is computed so that the accumulator layout (one query row
 //    per lane column) is directly the B operand of O^T = V^T.P^T: the
 //    probabilities never leave registers.
