@@ -36,6 +36,9 @@ constexpr int kTileKV = 64;           // kv tokens per iteration
 constexpr int kD = 128;               // head_dim of the MFMA kernel
 constexpr int kXcds = 8;              // MI355X: workgroup i runs on XCD i % 8
 constexpr int kLoadsPerThread = kTileKV * kD / 8 / kThreads;   // 16-byte K (and V) loads
+constexpr int kRowsPerLoad = kThreads / (kD / 8);   // tile rows one load round covers
+static_assert(kLoadsPerThread * kRowsPerLoad == kTileKV,
+              "a tile gather must cover exactly the kTileKV rows of an LDS buffer");
 
 struct PrefillArgs {
   const f16* q;
@@ -153,7 +156,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   // Tile registers: two sets, so that the gather of tile n + 2 is in flight
   // while tile n is computed and tile n + 1 waits to be parked in LDS. One
   // tile's loads take about one HBM round trip, longer than a tile's math.
-  // Thread tid moves dims 8 (tid % 16) .. +8 of tokens tid / 16 + 32 i.
+  // Thread tid moves dims 8 (tid % 16) .. +8 of tokens tid / 16 + kRowsPerLoad i.
   // The page ids of a gather are read one iteration ahead (pid), so no
   // lookup latency sits in front of the loads.
   const int ld_t = tid >> 4;
@@ -165,21 +168,17 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   auto read_ids = [&](int n0) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
-      const int tok = n0 + ld_t + 32 * i;
+      const int tok = n0 + ld_t + kRowsPerLoad * i;
       int p = -1;
-      if constexpr (STAGED) {
-        if (tok < kv_end) p = s_pg[tok >> a.page_shift];
-      } else {
-        if (tok < kv_end) p = pages[tok >> a.page_shift];
-        p = (p >= 0 && p < a.num_pages) ? p : -1;
-      }
-      pid[i] = p;
+      if (tok < kv_end) p = STAGED ? s_pg[tok >> a.page_shift] : pages[tok >> a.page_shift];
+      // An id becomes an address only if it is inside the pool.
+      pid[i] = uint32_t(p) < uint32_t(a.num_pages) ? p : -1;
     }
   };
   auto fetch = [&](int n0, Regs& rg) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
-      const int tok = n0 + ld_t + 32 * i;
+      const int tok = n0 + ld_t + kRowsPerLoad * i;
       const uint64_t off = uint64_t(uint32_t(pid[i])) * a.page_stride +
                            (uint32_t(tok & page_mask) * a.token_stride + ld_c);
       // Past-the-end tokens and bad ids read the zero row (cache-resident).
@@ -191,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   auto stash = [&](int buf, const Regs& rg) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
-      const int t = ld_t + 32 * i;
+      const int t = ld_t + kRowsPerLoad * i;
       *reinterpret_cast<f16x8*>(&sK[buf * kKHalves + t * kKPitch + ld_c]) = rg.k[i];
       *reinterpret_cast<f16x8*>(&sV[buf * kVHalves + t * kVPitch + ld_c]) = rg.v[i];
     }
