@@ -202,6 +202,9 @@ typedef struct {
   int32_t plan_ints;     /* int32 entries of the plan buffer in use       */
   int32_t num_qo_heads;  /* heads the plan was made for                    */
   int32_t max_kv_len;    /* longest kv_len among the planned rows          */
+  int32_t num_merge;     /* (tile, head) items whose KV range is split     */
+  int32_t num_slots;     /* partial-result slots of the split items        */
+  int32_t kv_chunk;      /* split length in tokens (0: nothing split)      */
 } kunserve_prefill_plan_info;
 
 /* Upper bound of the prefill plan length (int32 entries). */
@@ -211,12 +214,23 @@ int64_t kunserve_prefill_plan_bound(const int32_t* q_indptr_host,
 /* Host-side plan: tiles the ragged q rows (q_len[b] = q_indptr[b+1] -
  * q_indptr[b]) of every q head into tiles of tile_q rows, and orders the
  * (row, tile, head) items so that items reading the same K/V (same row and
- * KV head) run back to back on one XCD (one L2), longest first. */
+ * KV head) run back to back on one XCD (one L2), longest first. When the
+ * items cannot fill num_cus CUs twice over (0: 256 CUs), each item's KV
+ * range is split into chunks of kv_chunk tokens; split items write fp32
+ * partials to the workspace and are merged within kunserve_paged_prefill.
+ * Layout: num_tiles records of 6 ints (row or -1 for padding, first q row,
+ * q head, KV begin, KV end, partial slot or -1), then num_merge records of
+ * 5 ints (row, first q row, q head, first slot, splits). */
 int kunserve_prefill_plan(const int32_t* q_indptr_host,
                           const int32_t* kv_len_host, int32_t num_seqs,
                           int32_t num_qo_heads, int32_t num_kv_heads,
-                          int32_t* plan_host, int64_t plan_capacity,
+                          int32_t num_cus, int32_t* plan_host,
+                          int64_t plan_capacity,
                           kunserve_prefill_plan_info* info);
+
+/* Workspace bytes needed by kunserve_paged_prefill for this plan (0 when
+ * nothing is split). */
+int64_t kunserve_prefill_workspace_bytes(const kunserve_prefill_plan_info* info);
 
 /* Causal attention of the q_len[b] new rows of each sequence against its
  * kv_len[b] cached tokens (new ones already appended): q row i of
@@ -230,6 +244,7 @@ int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
                            int32_t num_qo_heads, float sm_scale,
                            const int32_t* plan_dev,
                            const kunserve_prefill_plan_info* info,
+                           void* workspace_dev, int64_t workspace_bytes,
                            kunserve_stream_t stream);
 
 #ifdef __cplusplus

@@ -21,6 +21,9 @@
 //    a wave's last visible position skip the math.
 //  * The plan places the workgroups that read the same K/V (same sequence
 //    and KV head) back to back on one XCD so that they share its L2.
+//  * Steps with too few q tiles to fill the device split each tile's KV
+//    range over several workgroups; those write fp32 partials (O, running
+//    max, sum) and a merge kernel combines them in split order.
 #include <algorithm>
 #include <vector>
 
@@ -55,10 +58,18 @@ struct PrefillArgs {
   const int32_t* indices;
   const int32_t* kv_len;
   const int32_t* q_indptr;
-  const int32_t* tiles;   // [num_tiles][3]: seq (-1: padding), first q row, q head
+  const int32_t* tiles;   // [num_tiles][kRec]: see kRec
+  float* part_o;          // [slots][kTileQ][kD] split partials, normalised
+  float* part_ml;         // [slots][kTileQ][2] running max (log2 units), sum
   int32_t ratio;
   float scale_log2;
 };
+
+// Plan record of one workgroup: seq (-1: padding), first q row, q head,
+// KV range [kv_lo, kv_hi) it attends over, partial slot (-1: writes out).
+constexpr int kRec = 6;
+// Merge record: seq, first q row, q head, first slot, number of splits.
+constexpr int kMergeRec = 5;
 
 // LDS layouts. Both tiles are row-major [token][dim] with padded rows, so
 // every operand address is a per-lane base plus an immediate offset:
@@ -99,11 +110,14 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   __shared__ __attribute__((aligned(16))) f16 sK[2 * kKHalves];
   __shared__ __attribute__((aligned(16))) f16 sV[2 * kVHalves];
 
-  const int32_t* item = a.tiles + 3 * blockIdx.x;
+  const int32_t* item = a.tiles + kRec * blockIdx.x;
   const int seq = item[0];
   if (seq < 0) return;   // padding workgroup (uniform: no barrier reached)
   const int q0 = item[1];
   const int hq = item[2];
+  const int kv_lo = item[3];   // a multiple of kTileKV
+  const int kv_hi = item[4];
+  const int slot = item[5];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -125,12 +139,13 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   const bool wave_active = q0 + wave * 32 < q_len;
   const int wave_first_pos = prefix + q0 + wave * 32;
   const int wave_last_pos = prefix + min(q0 + wave * 32 + 31, q_len - 1);
-  const int kv_end = prefix + min(q0 + kTileQ, q_len);   // exclusive
-  const int ntiles = (kv_end + kTileKV - 1) / kTileKV;
+  const int kv_end = min(prefix + min(q0 + kTileQ, q_len), kv_hi);   // exclusive
+  const int ntiles = (kv_end + kTileKV - 1) / kTileKV;   // tiles [kv_lo / kTileKV, ntiles)
+  const int pg_lo = kv_lo >> a.page_shift;   // first staged page
   if constexpr (STAGED) {
-    const int npg = kv_end > 0 ? ((kv_end - 1) >> a.page_shift) + 1 : 0;
+    const int npg = kv_end > kv_lo ? ((kv_end - 1) >> a.page_shift) + 1 - pg_lo : 0;
     for (int i = threadIdx.x; i < npg; i += kThreads) {
-      const int p = pages[i];
+      const int p = pages[pg_lo + i];
       s_pg[i] = (p >= 0 && p < a.num_pages) ? p : -1;
     }
     __syncthreads();
@@ -170,7 +185,8 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     for (int i = 0; i < kLoadsPerThread; ++i) {
       const int tok = n0 + ld_t + kRowsPerLoad * i;
       int p = -1;
-      if (tok < kv_end) p = STAGED ? s_pg[tok >> a.page_shift] : pages[tok >> a.page_shift];
+      if (tok < kv_end)
+        p = STAGED ? s_pg[(tok >> a.page_shift) - pg_lo] : pages[tok >> a.page_shift];
       // An id becomes an address only if it is inside the pool.
       pid[i] = uint32_t(p) < uint32_t(a.num_pages) ? p : -1;
     }
@@ -282,14 +298,14 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   // registers (loads issued one iteration earlier) and tile it + 2 is being
   // fetched into the other register set.
   Regs ra, rb;
-  read_ids(0);
-  fetch(0, ra);
-  read_ids(kTileKV);
-  fetch(kTileKV, rb);
+  read_ids(kv_lo);
+  fetch(kv_lo, ra);
+  read_ids(kv_lo + kTileKV);
+  fetch(kv_lo + kTileKV, rb);
   stash(0, ra);
-  read_ids(2 * kTileKV);
+  read_ids(kv_lo + 2 * kTileKV);
   __syncthreads();
-  for (int it = 0; it < ntiles; it += 2) {
+  for (int it = kv_lo / kTileKV; it < ntiles; it += 2) {
     // even tile: next tile in rb, fetch it + 2 into ra
     {
       const int n0 = it * kTileKV;
@@ -314,15 +330,86 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   lsum += __shfl_xor(lsum, 32);
   if (!row_ok) return;
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  f16* op = a.out + int64_t(qb + qrow) * a.o_tok + int64_t(hq) * a.o_head;
+  if (slot < 0) {
+    f16* op = a.out + int64_t(qb + qrow) * a.o_tok + int64_t(hq) * a.o_head;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f16x4 val = {f16(o[dt][4 * g] * inv), f16(o[dt][4 * g + 1] * inv),
+                           f16(o[dt][4 * g + 2] * inv), f16(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<f16x4*>(op + 32 * dt + 8 * g + 4 * h) = val;
+      }
+    return;
+  }
+  // Split: this KV range's normalised O, its running max and its sum. A row
+  // that sees no key of the range has sum 0 (weight 0 in the merge).
+  const int64_t prow = int64_t(slot) * kTileQ + (qrow - q0);
+  float* po = a.part_o + prow * kD;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const f16x4 val = {f16(o[dt][4 * g] * inv), f16(o[dt][4 * g + 1] * inv),
-                         f16(o[dt][4 * g + 2] * inv), f16(o[dt][4 * g + 3] * inv)};
-      *reinterpret_cast<f16x4*>(op + 32 * dt + 8 * g + 4 * h) = val;
+      const f32x4 val = {o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                         o[dt][4 * g + 3] * inv};
+      *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * g + 4 * h) = val;
     }
+  if (h == 0) {
+    a.part_ml[2 * prow] = m;
+    a.part_ml[2 * prow + 1] = lsum;
+  }
+}
+
+// Combines the splits of one (sequence, q tile, q head): weight of split j
+// = 2^(m_j - max m) * sum_j, taken in split order.
+struct MergeArgs {
+  const int32_t* merges;   // [num_merge][kMergeRec]
+  const float* part_o;
+  const float* part_ml;
+  const int32_t* q_indptr;
+  f16* out;
+  int64_t o_tok, o_head;
+};
+
+// Grid (merge record, block of kMergeRows rows); one thread per (row, 8 dims).
+constexpr int kMergeRows = 256 / (kD / 8);
+
+__global__ __launch_bounds__(256) void prefill_merge_kernel(MergeArgs a) {
+  const int32_t* rec = a.merges + kMergeRec * blockIdx.x;
+  const int seq = rec[0], q0 = rec[1], hq = rec[2], s0 = rec[3], n = rec[4];
+  const int qb = a.q_indptr[seq];
+  const int q_len = a.q_indptr[seq + 1] - qb;
+  {
+    const int row = blockIdx.y * kMergeRows + int(threadIdx.x) / (kD / 8);
+    const int c = int(threadIdx.x) % (kD / 8);
+    if (q0 + row >= q_len) return;
+    float mx = -INFINITY;
+    for (int j = 0; j < n; ++j) {
+      const int64_t pr = int64_t(s0 + j) * kTileQ + row;
+      if (a.part_ml[2 * pr + 1] > 0.f) mx = fmaxf(mx, a.part_ml[2 * pr]);
+    }
+    float wsum = 0.f, acc[8] = {};
+    for (int j = 0; j < n; ++j) {
+      const int64_t pr = int64_t(s0 + j) * kTileQ + row;
+      const float l = a.part_ml[2 * pr + 1];
+      if (!(l > 0.f)) continue;
+      const float w = fast_exp2(a.part_ml[2 * pr] - mx) * l;
+      wsum += w;
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(a.part_o + pr * kD + 8 * c);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(a.part_o + pr * kD + 8 * c + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[e] = fmaf(w, x0[e], acc[e]);
+        acc[4 + e] = fmaf(w, x1[e], acc[4 + e]);
+      }
+    }
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    f16* op = a.out + int64_t(qb + q0 + row) * a.o_tok + int64_t(hq) * a.o_head + 8 * c;
+    *reinterpret_cast<f16x4*>(op) = {f16(acc[0] * inv), f16(acc[1] * inv), f16(acc[2] * inv),
+                                     f16(acc[3] * inv)};
+    *reinterpret_cast<f16x4*>(op + 4) = {f16(acc[4] * inv), f16(acc[5] * inv), f16(acc[6] * inv),
+                                         f16(acc[7] * inv)};
+  }
 }
 
 // ------------------------------------------------------------ append
@@ -426,24 +513,35 @@ extern "C" int kunserve_append_kv(const kunserve_kv_pool* pool, int32_t layer,
   return KUNSERVE_OK;
 }
 
+// Splits: a step with fewer q-tile workgroups than CUs splits the KV range
+// of its tiles into about kSplitWaves workgroups per CU, each covering at
+// least kMinSplitTiles KV tiles (a multiple of kTileKV).
+constexpr int kSplitWaves = 2;
+constexpr int kMinSplitTiles = 4;
+constexpr int kMaxSplitItems = 2 * 1024;   // upper bound of the split target
+
 extern "C" int64_t kunserve_prefill_plan_bound(const int32_t* q_indptr_host, int32_t num_seqs,
                                                int32_t num_qo_heads) {
   if (num_seqs < 0 || num_qo_heads <= 0 || (num_seqs > 0 && !q_indptr_host)) return -1;
   int64_t tiles = 0;
   for (int32_t b = 0; b < num_seqs; ++b)
     tiles += (std::max(q_indptr_host[b + 1] - q_indptr_host[b], 0) + kTileQ - 1) / kTileQ;
-  // Worst case: every item on one XCD, the others padded to the same depth.
-  return 3 * kXcds * (tiles * num_qo_heads + 1);
+  const int64_t items = tiles * num_qo_heads;
+  // Splitting adds at most kMaxSplitItems workgroups; worst case every item
+  // on one XCD and the others padded to the same depth; one merge record per
+  // item.
+  return int64_t(kRec) * kXcds * (items + kMaxSplitItems + 1) + int64_t(kMergeRec) * items;
 }
 
 extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t* kv_len_host,
                                      int32_t num_seqs, int32_t num_qo_heads,
-                                     int32_t num_kv_heads, int32_t* plan_host,
+                                     int32_t num_kv_heads, int32_t num_cus, int32_t* plan_host,
                                      int64_t plan_capacity, kunserve_prefill_plan_info* info) {
   clear_error();
   KSV_CHECK_ARG(info && plan_host && num_seqs >= 0, "bad argument");
   KSV_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && num_qo_heads % num_kv_heads == 0,
                 "num_qo_heads %d not a multiple of num_kv_heads %d", num_qo_heads, num_kv_heads);
+  KSV_CHECK_ARG(num_cus >= 0, "num_cus %d < 0", num_cus);
   if (num_seqs > 0) KSV_CHECK_ARG(q_indptr_host && kv_len_host, "null q_indptr / kv_len");
   const int ratio = num_qo_heads / num_kv_heads;
   // A group = (sequence, KV head, q-tile range): its items (all `ratio` q
@@ -451,13 +549,25 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
   // work first. A (sequence, KV head) keeps all its tiles in one group
   // unless there are too few groups to spread over the XCDs.
   struct Group { int32_t seq, hkv, t0, t1; int64_t cost; };
-  int64_t n_pairs = 0;
+  int64_t n_pairs = 0, n_items = 0, kv_units = 0;
   for (int32_t b = 0; b < num_seqs; ++b) {
     const int32_t ql = q_indptr_host[b + 1] - q_indptr_host[b];
     KSV_CHECK_ARG(ql >= 0, "q_indptr not monotone at %d", b);
     KSV_CHECK_ARG(kv_len_host[b] >= ql, "kv_len[%d] = %d < q_len %d", b, kv_len_host[b], ql);
-    if (ql > 0) n_pairs += num_kv_heads;
+    if (ql == 0) continue;
+    n_pairs += num_kv_heads;
+    const int32_t prefix = kv_len_host[b] - ql;
+    for (int32_t q0 = 0; q0 < ql; q0 += kTileQ) {
+      n_items += num_qo_heads;
+      kv_units += int64_t(num_qo_heads) * ((prefix + std::min(q0 + kTileQ, ql) + kTileKV - 1) / kTileKV);
+    }
   }
+  // KV tiles per split (0: no split).
+  const int64_t cus = num_cus > 0 ? num_cus : 256;
+  const int64_t target = std::min<int64_t>(kSplitWaves * cus, kMaxSplitItems);
+  int64_t chunk = 0;
+  if (n_items > 0 && n_items < cus)
+    chunk = std::max<int64_t>(kMinSplitTiles, (kv_units + target - 1) / target);
   const bool split_tiles = n_pairs < 2 * kXcds;
   std::vector<Group> groups;
   for (int32_t b = 0; b < num_seqs; ++b) {
@@ -480,18 +590,52 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
   }
   std::stable_sort(groups.begin(), groups.end(),
                    [](const Group& x, const Group& y) { return x.cost > y.cost; });
+  // Items of a group, split range by split range (the items of one range
+  // read the same K/V), each range's tiles and heads together.
   std::vector<std::vector<int32_t>> lanes(kXcds);
+  std::vector<int32_t> merges;
   int64_t load[kXcds] = {};
+  int32_t slots = 0;
   for (const Group& g : groups) {
     const int x = int(std::min_element(load, load + kXcds) - load);
     load[x] += g.cost;
-    for (int32_t q0 = g.t0; q0 < g.t1; q0 += kTileQ)
-      for (int32_t hq = g.hkv * ratio; hq < (g.hkv + 1) * ratio; ++hq)
-        lanes[x].insert(lanes[x].end(), {g.seq, q0, hq});
+    const int32_t ql = q_indptr_host[g.seq + 1] - q_indptr_host[g.seq];
+    const int32_t prefix = kv_len_host[g.seq] - ql;
+    auto tile_end = [&](int32_t q0) { return prefix + std::min(q0 + kTileQ, ql); };
+    auto n_splits = [&](int32_t q0) {
+      const int64_t units = (tile_end(q0) + kTileKV - 1) / kTileKV;
+      return chunk > 0 ? int32_t((units + chunk - 1) / chunk) : 1;
+    };
+    int32_t max_splits = 1;
+    for (int32_t q0 = g.t0; q0 < g.t1; q0 += kTileQ) max_splits = std::max(max_splits, n_splits(q0));
+    // First slot of each (tile, head) that is split.
+    std::vector<int32_t> first_slot;
+    for (int32_t q0 = g.t0; q0 < g.t1; q0 += kTileQ) {
+      const int32_t n = n_splits(q0);
+      for (int32_t hq = g.hkv * ratio; hq < (g.hkv + 1) * ratio; ++hq) {
+        first_slot.push_back(n > 1 ? slots : -1);
+        if (n > 1) {
+          merges.insert(merges.end(), {g.seq, q0, hq, slots, n});
+          slots += n;
+        }
+      }
+    }
+    for (int32_t j = 0; j < max_splits; ++j) {
+      size_t k = 0;
+      for (int32_t q0 = g.t0; q0 < g.t1; q0 += kTileQ) {
+        const int32_t n = n_splits(q0);
+        for (int32_t hq = g.hkv * ratio; hq < (g.hkv + 1) * ratio; ++hq, ++k) {
+          if (j >= n) continue;
+          const int32_t lo = n > 1 ? int32_t(j * chunk * kTileKV) : 0;
+          const int32_t hi = (n > 1 && j + 1 < n) ? int32_t((j + 1) * chunk * kTileKV) : tile_end(q0);
+          lanes[x].insert(lanes[x].end(), {g.seq, q0, hq, lo, hi, n > 1 ? first_slot[k] + j : -1});
+        }
+      }
+    }
   }
   size_t depth = 0;
-  for (const auto& l : lanes) depth = std::max(depth, l.size() / 3);
-  const int64_t need = 3 * int64_t(depth) * kXcds;
+  for (const auto& l : lanes) depth = std::max(depth, l.size() / kRec);
+  const int64_t need = int64_t(kRec) * int64_t(depth) * kXcds + int64_t(merges.size());
   if (need > plan_capacity) {
     set_error("prefill plan needs %lld ints, capacity %lld", (long long)need,
               (long long)plan_capacity);
@@ -500,14 +644,16 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
   // Workgroup L runs on XCD L % 8: item i of XCD x goes to L = 8 i + x.
   for (size_t i = 0; i < depth; ++i)
     for (int x = 0; x < kXcds; ++x) {
-      int32_t* dst = plan_host + 3 * (i * kXcds + x);
-      if (3 * i < lanes[x].size()) {
-        std::copy(lanes[x].begin() + 3 * i, lanes[x].begin() + 3 * i + 3, dst);
+      int32_t* dst = plan_host + kRec * (i * kXcds + x);
+      if (kRec * i < lanes[x].size()) {
+        std::copy(lanes[x].begin() + kRec * i, lanes[x].begin() + kRec * (i + 1), dst);
       } else {
+        std::fill(dst, dst + kRec, 0);
         dst[0] = -1;
-        dst[1] = dst[2] = 0;
+        dst[5] = -1;
       }
     }
+  std::copy(merges.begin(), merges.end(), plan_host + int64_t(kRec) * depth * kXcds);
   info->num_tiles = int32_t(depth * kXcds);
   info->tile_q = kTileQ;
   info->plan_ints = int32_t(need);
@@ -518,7 +664,15 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
     if (ql > 0) max_kv = std::max(max_kv, kv_len_host[b]);
   }
   info->max_kv_len = max_kv;
+  info->num_merge = int32_t(merges.size() / kMergeRec);
+  info->num_slots = slots;
+  info->kv_chunk = int32_t(chunk * kTileKV);
   return KUNSERVE_OK;
+}
+
+extern "C" int64_t kunserve_prefill_workspace_bytes(const kunserve_prefill_plan_info* info) {
+  if (!info) return -1;
+  return int64_t(info->num_slots) * kTileQ * (kD + 2) * int64_t(sizeof(float));
 }
 
 extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
@@ -527,6 +681,7 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
                                       kunserve_tensor3* out, int32_t num_qo_heads,
                                       float sm_scale, const int32_t* plan_dev,
                                       const kunserve_prefill_plan_info* info,
+                                      void* workspace_dev, int64_t workspace_bytes,
                                       kunserve_stream_t stream) {
   clear_error();
   int rc = check_pool(pool, true);
@@ -555,6 +710,12 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   KSV_CHECK_ARG((reinterpret_cast<uintptr_t>(out->data) & 7) == 0 && out->token_stride % 4 == 0 &&
                     out->head_stride % 4 == 0,
                 "out must be 8-byte aligned with strides that are multiples of 4");
+  const int64_t ws_need = kunserve_prefill_workspace_bytes(info);
+  if (info->num_slots > 0 && (!workspace_dev || workspace_bytes < ws_need)) {
+    set_error("prefill workspace holds %lld bytes, %lld needed", (long long)workspace_bytes,
+              (long long)ws_need);
+    return KUNSERVE_ENOSPC;
+  }
   PrefillArgs a{};
   a.q = static_cast<const f16*>(q->data);
   a.q_tok = q->token_stride;
@@ -581,6 +742,8 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   a.kv_len = table->kv_len_dev;
   a.q_indptr = q_indptr_dev;
   a.tiles = plan_dev;
+  a.part_o = static_cast<float*>(workspace_dev);
+  a.part_ml = a.part_o ? a.part_o + int64_t(info->num_slots) * kTileQ * kD : nullptr;
   a.ratio = num_qo_heads / pool->num_kv_heads;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   const int64_t pages_needed = (int64_t(info->max_kv_len) + pool->page_size - 1) / pool->page_size;
@@ -591,5 +754,18 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
     paged_prefill_kernel<false><<<dim3(info->num_tiles), kThreads, 0,
                                   reinterpret_cast<hipStream_t>(stream)>>>(a);
   KSV_CHECK_LAUNCH();
+  if (info->num_merge > 0) {
+    MergeArgs m{};
+    m.merges = plan_dev + int64_t(kRec) * info->num_tiles;
+    m.part_o = a.part_o;
+    m.part_ml = a.part_ml;
+    m.q_indptr = q_indptr_dev;
+    m.out = a.out;
+    m.o_tok = a.o_tok;
+    m.o_head = a.o_head;
+    prefill_merge_kernel<<<dim3(info->num_merge, kTileQ / kMergeRows), 256, 0,
+                           reinterpret_cast<hipStream_t>(stream)>>>(m);
+    KSV_CHECK_LAUNCH();
+  }
   return KUNSERVE_OK;
 }

@@ -202,10 +202,12 @@ class DecodePlan:
 
 class PrefillPlan:
     """(row, q tile, q head) work items of the prefill rows, XCD-ordered
-    (kunserve_prefill_plan)."""
+    (kunserve_prefill_plan). Steps with too few items to fill the device
+    split each item's KV range; the merge runs inside paged_prefill."""
 
     def __init__(self, q_indptr_host: Sequence[int], kv_len_host: Sequence[int],
-                 num_qo_heads: int, num_kv_heads: int, device: torch.device):
+                 num_qo_heads: int, num_kv_heads: int, device: torch.device,
+                 num_cus: Optional[int] = None):
         qi = _i32(q_indptr_host)
         kv = _i32(kv_len_host)
         n = len(kv)
@@ -214,11 +216,15 @@ class PrefillPlan:
         cap = int(_lib.lib().kunserve_prefill_plan_bound(qi.ctypes.data, n, num_qo_heads))
         buf = np.zeros(max(cap, 3), dtype=np.int32)
         self.info = _lib.PrefillPlanInfo()
+        cus = num_cus if num_cus is not None else _num_cus(device)
         _lib.call("kunserve_prefill_plan", qi.ctypes.data, kv.ctypes.data if n else None, n,
-                  num_qo_heads, num_kv_heads, buf.ctypes.data, buf.size,
+                  num_qo_heads, num_kv_heads, cus, buf.ctypes.data, buf.size,
                   ctypes.byref(self.info))
         self.plan_host = buf[: self.info.plan_ints].copy()
         self.plan = torch.from_numpy(self.plan_host).to(device) if self.info.plan_ints else None
+
+    def workspace_bytes(self) -> int:
+        return int(_lib.lib().kunserve_prefill_workspace_bytes(ctypes.byref(self.info)))
 
 
 # ------------------------------------------------------------------ ops
@@ -341,15 +347,21 @@ def paged_decode(pool: KVPool, layer: int, table: PageTable, q: torch.Tensor, pl
 
 def paged_prefill(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Tensor,
                   q: torch.Tensor, plan: PrefillPlan, sm_scale: Optional[float] = None,
-                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  out: Optional[torch.Tensor] = None,
+                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Causal chunked-prefill attention of ragged q [num_tokens, Hq, D]."""
     if out is None:
         out = torch.empty_like(q)
     scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(pool.head_dim)
+    need = plan.workspace_bytes()
+    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=pool.device)
     qd, od = _tensor3(q), _tensor3(out)
     _lib.call("kunserve_paged_prefill", pool.desc(), layer, table.desc(), q_indptr.data_ptr(),
               ctypes.byref(qd), ctypes.byref(od), q.shape[1], ctypes.c_float(scale),
-              _ptr(plan.plan), ctypes.byref(plan.info), _stream_ptr(pool.device))
+              _ptr(plan.plan), ctypes.byref(plan.info), _ptr(workspace),
+              0 if workspace is None else workspace.numel() * workspace.element_size(),
+              _stream_ptr(pool.device))
     return out
 
 
@@ -419,6 +431,10 @@ class AttentionStep:
                 np.cumsum(q_lens[pre_rows], out=qi[1:])
             plan = PrefillPlan(qi, self.kv_len[pre_rows], num_qo_heads, pool.num_kv_heads, dev)
             self.prefill = _Subset(pre_rows, tokens, table, torch.from_numpy(qi).to(dev), plan)
+        # Scratch shared by every layer of the step (launches are serialised on one stream).
+        ws = max(self.decode.plan.workspace_bytes(pool.head_dim) if self.decode else 0,
+                 self.prefill.plan.workspace_bytes() if self.prefill else 0)
+        self.workspace = torch.empty(ws, dtype=torch.uint8, device=dev) if ws > 0 else None
 
     def run(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -431,18 +447,19 @@ class AttentionStep:
         if self.decode is not None:
             d = self.decode
             if d.tokens is None:
-                paged_decode(self.pool, layer, d.table, q, d.plan, self.scale, out=out)
+                paged_decode(self.pool, layer, d.table, q, d.plan, self.scale, out=out,
+                             workspace=self.workspace)
             else:
                 out[d.tokens] = paged_decode(self.pool, layer, d.table,
                                              q.index_select(0, d.tokens).contiguous(), d.plan,
-                                             self.scale)
+                                             self.scale, workspace=self.workspace)
         if self.prefill is not None:
             p = self.prefill
             if p.tokens is None:
                 paged_prefill(self.pool, layer, p.table, p.q_indptr, q, p.plan, self.scale,
-                              out=out)
+                              out=out, workspace=self.workspace)
             else:
                 out[p.tokens] = paged_prefill(self.pool, layer, p.table, p.q_indptr,
                                               q.index_select(0, p.tokens).contiguous(), p.plan,
-                                              self.scale)
+                                              self.scale, workspace=self.workspace)
         return out

@@ -77,13 +77,51 @@ def test_decode_plan_rejects_bad_arguments():
     assert e.value.code == _lib.ENOSPC
 
 
-def _prefill_plan(q_indptr, kv, hq, hkv):
+def _prefill_plan(q_indptr, kv, hq, hkv, num_cus=256):
     cap = _lib.lib().kunserve_prefill_plan_bound(q_indptr.ctypes.data, len(kv), hq)
-    buf = np.zeros(cap, dtype=np.int32)
+    buf = np.full(cap, -7, dtype=np.int32)
     info = _lib.PrefillPlanInfo()
     _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, kv.ctypes.data, len(kv), hq, hkv,
-              buf.ctypes.data, cap, ctypes.byref(info))
-    return info, buf[:info.plan_ints].reshape(-1, 3)
+              num_cus, buf.ctypes.data, cap, ctypes.byref(info))
+    items = buf[:6 * info.num_tiles].reshape(-1, 6)
+    merges = buf[6 * info.num_tiles:info.plan_ints].reshape(-1, 5)
+    return info, items, merges
+
+
+def _check_prefill_plan(q_indptr, q_lens, kv, hq, hkv, info, items, merges):
+    """Every (row, q tile, q head) covers its visible KV range [0, tile end)
+    exactly once, split ranges are tile-aligned and contiguous, slots are
+    distinct, and each split item has one merge record."""
+    tq = info.tile_q
+    n = len(kv)
+    assert info.num_tiles % 8 == 0 and info.num_tiles == len(items)
+    assert np.all(items[items[:, 0] < 0][:, 5] == -1)
+    real = items[items[:, 0] >= 0]
+    ranges = {}
+    for b, q0, h, lo, hi, slot in real.tolist():
+        ranges.setdefault((b, q0, h), []).append((lo, hi, slot))
+    want = {(b, q0, h) for b in range(n) for q0 in range(0, int(q_lens[b]), tq)
+            for h in range(hq)}
+    assert set(ranges) == want
+    slots = []
+    merged = {(b, q0, h): (s0, cnt) for b, q0, h, s0, cnt in merges.tolist()}
+    assert len(merged) == len(merges) == info.num_merge
+    for (b, q0, h), rs in ranges.items():
+        end = int(kv[b]) - int(q_lens[b]) + min(q0 + tq, int(q_lens[b]))
+        rs.sort()
+        assert rs[0][0] == 0 and rs[-1][1] == end
+        for (lo1, hi1, _), (lo2, _, _) in zip(rs, rs[1:]):
+            assert hi1 == lo2 and hi1 % 64 == 0
+        if len(rs) == 1:
+            assert rs[0][2] == -1 and (b, q0, h) not in merged
+        else:
+            s0, cnt = merged[(b, q0, h)]
+            assert cnt == len(rs) and [r[2] for r in rs] == list(range(s0, s0 + cnt))
+            assert all(hi - lo >= 64 * 4 or hi == end for lo, hi, _ in rs)
+            slots += [r[2] for r in rs]
+    assert sorted(slots) == list(range(info.num_slots))
+    ws = _lib.lib().kunserve_prefill_workspace_bytes(ctypes.byref(info))
+    assert ws == info.num_slots * tq * (128 + 2) * 4
 
 
 @pytest.mark.parametrize("hq,hkv,n", [(4, 4, 3), (8, 2, 3), (32, 32, 16), (1, 1, 1)])
@@ -92,20 +130,39 @@ def test_prefill_plan_covers_every_tile_once(hq, hkv, n):
     q_lens = rng.integers(0, 900, n)
     q_indptr = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
     kv = (q_lens + rng.integers(0, 3000, n)).astype(np.int32)
-    info, items = _prefill_plan(q_indptr, kv, hq, hkv)
-    tq = info.tile_q
-    assert info.num_tiles % 8 == 0 and info.num_tiles == len(items)
-    real = items[items[:, 0] >= 0]
-    want = {(b, q0, h) for b in range(n) for q0 in range(0, int(q_lens[b]), tq)
-            for h in range(hq)}
-    assert set(map(tuple, real.tolist())) == want and len(real) == len(want)
-    # items that read the same K/V (row, KV head) sit on one XCD unless split
+    info, items, merges = _prefill_plan(q_indptr, kv, hq, hkv)
+    _check_prefill_plan(q_indptr, q_lens, kv, hq, hkv, info, items, merges)
+    # items that read the same K/V (row, KV head) sit on one XCD
     xcd = {}
-    for L, (b, q0, h) in enumerate(items.tolist()):
+    for L, (b, q0, h, lo, hi, slot) in enumerate(items.tolist()):
         if b >= 0:
             xcd.setdefault((b, h // (hq // hkv)), set()).add(L % 8)
     if len(xcd) >= 16:
         assert all(len(v) == 1 for v in xcd.values())
+
+
+@pytest.mark.parametrize("num_cus", [0, 64, 256, 1024])
+def test_prefill_plan_splits_small_steps(num_cus):
+    """A step with fewer q-tile items than CUs (one long row: the last step
+    of a chunked prefill, 64 items) is split over about 2 x CUs workgroups;
+    a step with enough items is not."""
+    q_lens = np.array([512], dtype=np.int64)
+    kv = np.array([4806], dtype=np.int32)
+    q_indptr = np.array([0, 512], dtype=np.int32)
+    info, items, merges = _prefill_plan(q_indptr, kv, 32, 32, num_cus)
+    _check_prefill_plan(q_indptr, q_lens, kv, 32, 32, info, items, merges)
+    cus = num_cus or 256
+    real = int((items[:, 0] >= 0).sum())
+    if cus <= 64:
+        assert info.num_merge == 0 and real == 64
+    else:
+        assert info.num_merge == 64 and info.kv_chunk % 64 == 0 and info.kv_chunk >= 256
+        assert cus <= real <= 2 * cus + 64
+    big = np.full(16, 512, dtype=np.int64)
+    qi = np.concatenate([[0], np.cumsum(big)]).astype(np.int32)
+    kvb = np.full(16, 2048, dtype=np.int32)
+    info, items, merges = _prefill_plan(qi, kvb, 32, 32, 256)
+    assert info.num_merge == 0 and info.num_slots == 0 and info.kv_chunk == 0
 
 
 def test_prefill_plan_rejects_short_kv():
@@ -114,7 +171,7 @@ def test_prefill_plan_rejects_short_kv():
     buf = np.zeros(64, dtype=np.int32)
     info = _lib.PrefillPlanInfo()
     with pytest.raises(_lib.KunserveError):
-        _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, bad.ctypes.data, 3, 4, 4,
+        _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, bad.ctypes.data, 3, 4, 4, 0,
                   buf.ctypes.data, 64, ctypes.byref(info))
 
 

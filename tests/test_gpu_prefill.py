@@ -71,6 +71,32 @@ def test_prefill_matches_oracle(device, hq, hkv, ps):
     assert max_abs(out, want) <= ATOL
 
 
+@pytest.mark.parametrize("ps", [16, 64])
+def test_prefill_split_kv_matches_oracle(device, ps):
+    """Split KV ranges (a plan made for 1024 CUs splits every tile of this
+    small batch) merge to the oracle and to the unsplit result."""
+    rng = np.random.default_rng(40 + ps)
+    q_lens = [1, 77, 256, 300, 512]
+    prefixes = [700, 0, 1500, 33, 2048]
+    npg = 600 if ps == 16 else 160
+    kv, indptr, indices, q_indptr = make_rows(rng, q_lens, prefixes, ps, npg)
+    pool = random_pool(npg, 1, 4, ps, 128, device, 41)
+    T = int(q_indptr[-1])
+    q = random_tensor((T, 8, 128), device, 42)
+    table = table_from_csr(indptr, indices, kv, device)
+    qi = torch.from_numpy(q_indptr).to(device)
+    split = PrefillPlan(q_indptr, kv, 8, 4, device, num_cus=1024)
+    assert split.info.num_merge > 0 and split.info.kv_chunk >= 256
+    whole = PrefillPlan(q_indptr, kv, 8, 4, device, num_cus=1)
+    assert whole.info.num_merge == 0
+    out_s = paged_prefill(pool, 0, table, qi, q, split)
+    out_w = paged_prefill(pool, 0, table, qi, q, whole)
+    torch.cuda.synchronize()
+    assert max_abs(out_s, out_w.float()) <= 1e-3
+    want = oracle_prefill(pool, 0, q, q_indptr, indptr, indices, kv)
+    assert max_abs(out_s, want) <= ATOL
+
+
 def test_prefill_one_token_rows_equal_decode(device):
     """A one-token prefill row is a decode row (use_tensor_cores path)."""
     rng = np.random.default_rng(7)
