@@ -307,6 +307,28 @@ def bench_prefill(args, device):
             if timer:
                 timer.stop(s)
 
+    # The fused RoPE + append prologue over the same steps: HBM-bound, bytes =
+    # q read and written, k and v read, rotated k and v written.
+    inv_freq = ks.rope_inv_freq(w.head_dim, 10000.0, device)
+    rope_bytes = 0
+    for table, qi, plan, q, k, v, out in steps:
+        T = q.shape[0]
+        rope_bytes += 2 * T * w.num_qo_heads * w.head_dim * 2 + 4 * T * w.num_kv_heads * w.head_dim * 2
+
+    def run_rope(timer=None):
+        for table, qi, plan, q, k, v, out in steps:
+            s = timer.start() if timer else None
+            ks.rope_append_kv(pool, 0, table, qi, q, k, v, inv_freq)
+            if timer:
+                timer.stop(s)
+
+    run_rope()
+    rope_timer = LaunchTimer()
+    run_rope(rope_timer)
+    rope_ms = rope_timer.mean_ms() * len(steps)
+    log(f"rope + append prologue: {rope_ms:.3f} ms for the 8 steps = "
+        f"{rope_bytes / (rope_ms * 1e-3) / 1e9:.1f} GB/s")
+
     reps = max(1, args.steps // 4)
     for _ in range(max(1, args.warmup)):
         run()
@@ -328,7 +350,9 @@ def bench_prefill(args, device):
         f"of fp16 MFMA peak)")
     return {"workload": w.name, "causal_tflop": flops / 1e12, "steps": len(steps),
             "ms_with_append": elapsed * 1e3, "attention_ms": attn_ms, "tflops": tflops,
-            "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS}
+            "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS,
+            "rope_append": {"ms": rope_ms, "bytes": rope_bytes,
+                            "gbs": rope_bytes / (rope_ms * 1e-3) / 1e9}}
 
 
 def load_traffic():

@@ -151,6 +151,26 @@ int kunserve_append_kv(const kunserve_kv_pool* pool, int32_t layer,
                        const kunserve_tensor3* v_new,
                        kunserve_stream_t stream);
 
+/* Fused attention prologue of a step: rotary position embedding of q (in
+ * place, all num_qo_heads heads) and of k_new, then the append of the
+ * rotated k and of v_new into the pages, as kunserve_append_kv. Token i of
+ * row b sits at position kv_len[b] - q_len[b] + i (kunserve/request.py:
+ * 447-462). inv_freq_dev holds head_dim / 2 fp32 frequencies (Llama:
+ * theta^(-2j / head_dim)); the angle of pair j is the fp32 product
+ * position * inv_freq[j]. Pairs are (j, j + head_dim / 2) ("rotate half"),
+ * or (2j, 2j + 1) when interleave is non-zero. fp32 rotation, one rounding.
+ * No reference counterpart: the rotation sits inside the native LlamaOp,
+ * whose source the reference does not ship; this is the prologue that
+ * LlamaOp.pforward runs before attention (kunserve/worker.py:298-312). */
+int kunserve_rope_append_kv(const kunserve_kv_pool* pool, int32_t layer,
+                            const kunserve_page_table* table,
+                            const int32_t* q_indptr_dev, int32_t num_tokens,
+                            kunserve_tensor3* q, int32_t num_qo_heads,
+                            const kunserve_tensor3* k_new,
+                            const kunserve_tensor3* v_new,
+                            const float* inv_freq_dev, int32_t interleave,
+                            kunserve_stream_t stream);
+
 /* ---------------------------------------------- decode attention (A4) */
 
 typedef struct {

@@ -13,12 +13,13 @@ from . import _lib
 from .llama_op import LlamaOp
 from .paged_kv import (AttentionStep, DecodePlan, KVPool, PageTable, PrefillPlan, append_kv,
                        copy_blocks, csr_from_lists, kv_lens_for_step, kv_pack, kv_scatter,
-                       paged_decode, paged_prefill, swap)
+                       paged_decode, paged_prefill, rope_append_kv, rope_inv_freq, swap)
 
 __all__ = [
     "AttentionStep", "DecodePlan", "KVPool", "LlamaOp", "PageTable", "PrefillPlan",
     "append_kv", "copy_blocks", "csr_from_lists", "kv_lens_for_step", "kv_pack",
-    "kv_scatter", "paged_decode", "paged_prefill", "swap", "library_path",
+    "kv_scatter", "paged_decode", "paged_prefill", "rope_append_kv", "rope_inv_freq", "swap",
+    "library_path",
 ]
 
 

@@ -70,6 +70,9 @@ SIGNATURES = {
                                      c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "kunserve_append_kv": (c_int, [POINTER(KVPool), c_int32, POINTER(PageTable), c_void_p,
                                    c_int32, POINTER(Tensor3), POINTER(Tensor3), c_void_p]),
+    "kunserve_rope_append_kv": (c_int, [POINTER(KVPool), c_int32, POINTER(PageTable), c_void_p,
+                                        c_int32, POINTER(Tensor3), c_int32, POINTER(Tensor3),
+                                        POINTER(Tensor3), c_void_p, c_int32, c_void_p]),
     "kunserve_decode_plan_bound": (c_int64, [c_void_p, c_int32]),
     "kunserve_decode_plan": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
                                      c_void_p, c_int64, POINTER(DecodePlanInfo)]),

@@ -460,10 +460,188 @@ __global__ __launch_bounds__(256) void append_kv_kernel(AppendArgs a) {
   store_f16x8(a.v + dst, load_f16x8(a.v_new + int64_t(tok) * a.v_tok + int64_t(head) * a.v_head + dc * 8));
 }
 
+// Fused prologue of a step: rotary position embedding of q (in place) and
+// of the new k, and the append of the rotated k and of v into the pages.
+// One thread per (token, head slot, 16 dims): head slots [0, Hq) are q
+// heads, [Hq, Hq + Hkv) are KV heads (k rotated and written, v copied).
+// Rotation pairs are (j, j + D/2) with the thread's dims 8c..8c+7 and
+// D/2 + 8c..+7, or (2j, 2j + 1) with dims 16c..16c+15 when interleaved.
+// Angles are the fp32 product position * inv_freq[j]; the rotation runs in
+// fp32 and rounds once.
+struct RopeArgs {
+  f16* q;
+  int64_t q_tok, q_head;
+  const f16* k_new;
+  const f16* v_new;
+  int64_t k_tok, k_head, v_tok, v_head;
+  f16* k;   // pool at the layer
+  f16* v;
+  int64_t page_stride, head_stride, token_stride;
+  int32_t num_pages;
+  int32_t page_shift;
+  const int32_t* indptr;
+  const int32_t* indices;
+  const int32_t* kv_len;
+  const int32_t* q_indptr;
+  const float* inv_freq;   // [D / 2]
+  int32_t num_seqs;
+  int32_t num_tokens;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t interleave;
+};
+
+__device__ __forceinline__ void rope_pair(float& a, float& b, float c, float s) {
+  const float x = a, y = b;
+  a = fmaf(x, c, -y * s);
+  b = fmaf(y, c, x * s);
+}
+
+__global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
+  const int units = a.head_dim / 16;   // 16-dim units per head
+  const int64_t per_tok = int64_t(a.num_qo_heads + a.num_kv_heads) * units;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= int64_t(a.num_tokens) * per_tok) return;
+  const int tok = int(idx / per_tok);
+  if (tok >= a.q_indptr[a.num_seqs]) return;   // tokens not owned by any row
+  const int rem = int(idx % per_tok);
+  const int slot = rem / units;
+  const int c = rem % units;
+  int lo = 0, hi = a.num_seqs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a.q_indptr[mid] <= tok) lo = mid; else hi = mid - 1;
+  }
+  const int b = lo;
+  const int q_len = a.q_indptr[b + 1] - a.q_indptr[b];
+  const int pos = a.kv_len[b] - q_len + (tok - a.q_indptr[b]);
+  if (pos < 0 || pos >= a.kv_len[b]) return;
+
+  // The thread's two 8-dim halves and the inv_freq index of each pair.
+  const int half = a.head_dim / 2;
+  const int d0 = a.interleave ? 16 * c : 8 * c;
+  const int d1 = a.interleave ? 16 * c + 8 : half + 8 * c;
+  const int f0 = 8 * c;   // first of the thread's 8 pairs
+  float cs[8], sn[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float ang = float(pos) * a.inv_freq[f0 + j];
+    sincosf(ang, &sn[j], &cs[j]);
+  }
+  auto rotate = [&](const f16x8& x0, const f16x8& x1, f16x8& y0, f16x8& y1) {
+    float u[16];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      u[e] = float(x0[e]);
+      u[8 + e] = float(x1[e]);
+    }
+    if (a.interleave) {
+      // dims 16c + 2j, 16c + 2j + 1 hold pair 8c + j
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rope_pair(u[2 * j], u[2 * j + 1], cs[j], sn[j]);
+    } else {
+      // dims 8c + j and D/2 + 8c + j hold pair 8c + j
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rope_pair(u[j], u[8 + j], cs[j], sn[j]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      y0[e] = f16(u[e]);
+      y1[e] = f16(u[8 + e]);
+    }
+  };
+
+  if (slot < a.num_qo_heads) {
+    f16* qp = a.q + int64_t(tok) * a.q_tok + int64_t(slot) * a.q_head;
+    f16x8 y0, y1;
+    rotate(load_f16x8(qp + d0), load_f16x8(qp + d1), y0, y1);
+    store_f16x8(qp + d0, y0);
+    store_f16x8(qp + d1, y1);
+    return;
+  }
+  const int head = slot - a.num_qo_heads;
+  const int p = a.indices[a.indptr[b] + (pos >> a.page_shift)];
+  if (p < 0 || p >= a.num_pages) return;
+  const int64_t dst = int64_t(p) * a.page_stride + int64_t(head) * a.head_stride +
+                      int64_t(pos & ((1 << a.page_shift) - 1)) * a.token_stride;
+  const f16* kp = a.k_new + int64_t(tok) * a.k_tok + int64_t(head) * a.k_head;
+  const f16* vp = a.v_new + int64_t(tok) * a.v_tok + int64_t(head) * a.v_head;
+  f16x8 y0, y1;
+  rotate(load_f16x8(kp + d0), load_f16x8(kp + d1), y0, y1);
+  store_f16x8(a.k + dst + d0, y0);
+  store_f16x8(a.k + dst + d1, y1);
+  store_f16x8(a.v + dst + d0, load_f16x8(vp + d0));
+  store_f16x8(a.v + dst + d1, load_f16x8(vp + d1));
+}
+
 }  // namespace
 }  // namespace kunserve
 
 using namespace kunserve;
+
+extern "C" int kunserve_rope_append_kv(const kunserve_kv_pool* pool, int32_t layer,
+                                       const kunserve_page_table* table,
+                                       const int32_t* q_indptr_dev, int32_t num_tokens,
+                                       kunserve_tensor3* q, int32_t num_qo_heads,
+                                       const kunserve_tensor3* k_new,
+                                       const kunserve_tensor3* v_new, const float* inv_freq_dev,
+                                       int32_t interleave, kunserve_stream_t stream) {
+  clear_error();
+  int rc = check_pool(pool, true);
+  if (rc) return rc;
+  KSV_CHECK_ARG(table && q && k_new && v_new, "null argument");
+  KSV_CHECK_ARG(layer >= 0 && layer < pool->num_layers, "layer %d outside [0, %d)", layer,
+                pool->num_layers);
+  KSV_CHECK_ARG(num_tokens >= 0, "num_tokens < 0");
+  KSV_CHECK_ARG(num_qo_heads > 0 && num_qo_heads % pool->num_kv_heads == 0,
+                "num_qo_heads %d not a multiple of num_kv_heads %d", num_qo_heads,
+                pool->num_kv_heads);
+  KSV_CHECK_ARG(pool->head_dim % 16 == 0, "head_dim %d is not a multiple of 16", pool->head_dim);
+  if (num_tokens == 0 || table->num_seqs == 0) return KUNSERVE_OK;
+  KSV_CHECK_ARG(q_indptr_dev && table->indptr_dev && table->indices_dev && table->kv_len_dev &&
+                    inv_freq_dev,
+                "null table array or inv_freq");
+  for (const kunserve_tensor3* t : {static_cast<const kunserve_tensor3*>(q), k_new, v_new})
+    KSV_CHECK_ARG(t->data && aligned16(t->data) && t->token_stride % 8 == 0 &&
+                      t->head_stride % 8 == 0,
+                  "q / k_new / v_new must be 16-byte aligned with strides that are multiples of 8");
+  RopeArgs a{};
+  a.q = static_cast<f16*>(q->data);
+  a.q_tok = q->token_stride;
+  a.q_head = q->head_stride;
+  a.k_new = static_cast<const f16*>(k_new->data);
+  a.v_new = static_cast<const f16*>(v_new->data);
+  a.k_tok = k_new->token_stride;
+  a.k_head = k_new->head_stride;
+  a.v_tok = v_new->token_stride;
+  a.v_head = v_new->head_stride;
+  a.k = static_cast<f16*>(pool->k) + int64_t(layer) * pool->layer_stride;
+  a.v = static_cast<f16*>(pool->v) + int64_t(layer) * pool->layer_stride;
+  a.page_stride = pool->page_stride;
+  a.head_stride = pool->head_stride;
+  a.token_stride = pool->token_stride;
+  a.num_pages = int32_t(pool->num_pages);
+  a.page_shift = __builtin_ctz(pool->page_size);
+  a.indptr = table->indptr_dev;
+  a.indices = table->indices_dev;
+  a.kv_len = table->kv_len_dev;
+  a.q_indptr = q_indptr_dev;
+  a.inv_freq = inv_freq_dev;
+  a.num_seqs = table->num_seqs;
+  a.num_tokens = num_tokens;
+  a.num_qo_heads = num_qo_heads;
+  a.num_kv_heads = pool->num_kv_heads;
+  a.head_dim = pool->head_dim;
+  a.interleave = interleave != 0;
+  const int64_t threads =
+      int64_t(num_tokens) * (num_qo_heads + pool->num_kv_heads) * (pool->head_dim / 16);
+  const int64_t blocks = (threads + 255) / 256;
+  KSV_CHECK_ARG(blocks < (int64_t(1) << 31), "rope append too large for one launch");
+  rope_append_kernel<<<dim3(unsigned(blocks)), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
+  KSV_CHECK_LAUNCH();
+  return KUNSERVE_OK;
+}
 
 extern "C" int kunserve_append_kv(const kunserve_kv_pool* pool, int32_t layer,
                                   const kunserve_page_table* table, const int32_t* q_indptr_dev,

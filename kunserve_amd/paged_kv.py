@@ -322,6 +322,39 @@ def append_kv(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Tensor
               k_new.shape[0], ctypes.byref(kd), ctypes.byref(vd), _stream_ptr(pool.device))
 
 
+def rope_inv_freq(head_dim: int, theta: float = 10000.0,
+                  device: Optional[torch.device] = None) -> torch.Tensor:
+    """Llama rotary frequencies theta^(-2j / head_dim), j < head_dim / 2, in
+    float32 (the table kunserve_rope_append_kv takes)."""
+    inv = 1.0 / (np.float32(theta) ** (np.arange(0, head_dim, 2, dtype=np.float32)
+                                       / np.float32(head_dim)))
+    t = torch.from_numpy(inv.astype(np.float32))
+    return t.to(device) if device is not None else t
+
+
+def rope_append_kv(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Tensor,
+                   q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                   inv_freq: torch.Tensor, interleave: bool = False) -> torch.Tensor:
+    """The attention prologue of one layer: rotates q in place and k_new at
+    each new token's position, and writes the rotated k and v_new into their
+    pages. Returns q."""
+    if k_new.shape != v_new.shape or k_new.shape[1:] != (pool.num_kv_heads, pool.head_dim):
+        raise ValueError(f"k_new / v_new must be [tokens, {pool.num_kv_heads}, {pool.head_dim}]")
+    if q.shape[0] != k_new.shape[0] or q.shape[2] != pool.head_dim:
+        raise ValueError(f"q {tuple(q.shape)} does not match k_new {tuple(k_new.shape)}")
+    if q_indptr.numel() != table.num_seqs + 1:
+        raise ValueError("q_indptr must have num_seqs + 1 entries")
+    if (inv_freq.dtype != torch.float32 or inv_freq.numel() != pool.head_dim // 2
+            or inv_freq.device != q.device):
+        raise ValueError(f"inv_freq must be {pool.head_dim // 2} float32 values on {q.device}")
+    inv_freq = inv_freq.contiguous()
+    qd, kd, vd = _tensor3(q), _tensor3(k_new), _tensor3(v_new)
+    _lib.call("kunserve_rope_append_kv", pool.desc(), layer, table.desc(), q_indptr.data_ptr(),
+              k_new.shape[0], ctypes.byref(qd), q.shape[1], ctypes.byref(kd), ctypes.byref(vd),
+              inv_freq.data_ptr(), int(bool(interleave)), _stream_ptr(pool.device))
+    return q
+
+
 def paged_decode(pool: KVPool, layer: int, table: PageTable, q: torch.Tensor, plan: DecodePlan,
                  sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -437,11 +470,21 @@ class AttentionStep:
         self.workspace = torch.empty(ws, dtype=torch.uint8, device=dev) if ws > 0 else None
 
     def run(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-            out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """q [num_tokens, Hq, D], k/v [num_tokens, Hkv, D] -> out [num_tokens, Hq, D]."""
+            out: Optional[torch.Tensor] = None,
+            rope: Optional[tuple] = None) -> torch.Tensor:
+        """q [num_tokens, Hq, D], k/v [num_tokens, Hkv, D] -> out [num_tokens, Hq, D].
+
+        With rope = (inv_freq, interleave), q and k are first rotated at their
+        positions (q in place) by the fused prologue kernel; without it they
+        are taken as already rotated."""
         if q.shape[0] != self.num_tokens or k.shape[0] != self.num_tokens:
             raise ValueError(f"expected {self.num_tokens} tokens, got q {q.shape[0]}, k {k.shape[0]}")
-        append_kv(self.pool, layer, self.table, self.q_indptr, k, v)
+        if rope is not None:
+            inv_freq, interleave = rope
+            rope_append_kv(self.pool, layer, self.table, self.q_indptr, q, k, v, inv_freq,
+                           interleave)
+        else:
+            append_kv(self.pool, layer, self.table, self.q_indptr, k, v)
         if out is None:
             out = torch.empty_like(q)
         if self.decode is not None:

@@ -13,6 +13,10 @@ reference's Python call sites, in plain numpy (float64 by default):
                       heads kunserve/models.py:55-56, page size kunserve/models.py:57
   prefill_attention   LlamaOp.pforward prefill rows     kunserve/request.py:368-391,428-462
   append_kv           K/V append into pages             kunserve/block_manager.py:786-795
+  rope, rope_append_kv  rotary positions + append (the pforward prologue; positions
+                      from the A3 rule, kunserve/request.py:447-462; the rotation itself
+                      is inside the absent native LlamaOp, so its pairing convention is
+                      taken as a parameter: parity unpinned beyond the closed forms)
   copy_blocks         LlamaOp.local_copy_blocks         kunserve/worker.py:818-823
   swap                swapping_ops.swap                 kunserve/worker.py:646-650,673-681
   kv_pack/kv_scatter  kv_exchange phases 1 and 3        kunserve/flash_backend.py:857-1022
@@ -129,6 +133,52 @@ def append_kv(k_pool: np.ndarray, v_pool: np.ndarray, layer: int, indptr: np.nda
             page = int(indices[indptr[b] + pos // ps])
             k_pool[page, layer, :, pos % ps] = k_new[q0 + i]
             v_pool[page, layer, :, pos % ps] = v_new[q0 + i]
+
+
+def rope(x: np.ndarray, pos: np.ndarray, inv_freq: np.ndarray, interleave: bool) -> np.ndarray:
+    """Rotary position embedding of x [T, H, D] at positions pos [T].
+
+    The angle of pair j is the float32 product pos * inv_freq[j] (the rounding
+    every fp32 implementation shares); cos, sin and the rotation are then
+    evaluated in float64. Pairs are (j, j + D/2) (rotate_half) or, with
+    interleave, (2j, 2j + 1). Returns float64."""
+    x = np.asarray(x, dtype=np.float64)
+    d = x.shape[-1]
+    ang = (np.asarray(pos).astype(np.float32)[:, None] * np.asarray(inv_freq, np.float32)[None, :])
+    c = np.cos(ang.astype(np.float64))[:, None, :]
+    s = np.sin(ang.astype(np.float64))[:, None, :]
+    if interleave:
+        a, b = x[..., 0::2], x[..., 1::2]
+        out = np.empty_like(x)
+        out[..., 0::2] = a * c - b * s
+        out[..., 1::2] = b * c + a * s
+        return out
+    a, b = x[..., : d // 2], x[..., d // 2:]
+    return np.concatenate([a * c - b * s, b * c + a * s], axis=-1)
+
+
+def token_positions(kv_len: np.ndarray, q_indptr: np.ndarray) -> np.ndarray:
+    """Position of every new token: row b's token i sits at kv_len[b] - q_len[b] + i
+    (kunserve/request.py:447-462)."""
+    out = []
+    for b in range(len(kv_len)):
+        q0, q1 = int(q_indptr[b]), int(q_indptr[b + 1])
+        out.extend(range(int(kv_len[b]) - (q1 - q0), int(kv_len[b])))
+    return np.asarray(out, dtype=np.int64)
+
+
+def rope_append_kv(k_pool: np.ndarray, v_pool: np.ndarray, layer: int, indptr: np.ndarray,
+                   indices: np.ndarray, kv_len: np.ndarray, q_indptr: np.ndarray,
+                   q: np.ndarray, k_new: np.ndarray, v_new: np.ndarray,
+                   inv_freq: np.ndarray, interleave: bool) -> np.ndarray:
+    """The attention prologue of a step: rotate q and the new k at their token
+    positions, append the rotated k and v into the pages (in place). Returns
+    the rotated q, rounded to the pool dtype."""
+    pos = token_positions(kv_len, q_indptr)
+    q_rot = rope(q, pos, inv_freq, interleave).astype(k_pool.dtype)
+    k_rot = rope(k_new, pos, inv_freq, interleave).astype(k_pool.dtype)
+    append_kv(k_pool, v_pool, layer, indptr, indices, kv_len, q_indptr, k_rot, v_new)
+    return q_rot
 
 
 def copy_blocks(pool: np.ndarray, src: Sequence[int], dst: Sequence[int]) -> None:

@@ -254,3 +254,92 @@ def test_fused_page_ids():
     assert ref.kept_page_id(3, 12, 3, 2) == 11
     # the kept id is one of the fused ids of that page
     assert ref.kept_page_id(3, 12, 3, 2) in ref.fused_page_ids(3, 4, 3)
+
+
+# ------------------------------------------------------------------ rope
+
+def _hf_rotate_half(x, pos, inv_freq):
+    """The Hugging Face Llama form: x * cos + rotate_half(x) * sin with
+    cos/sin of cat(freqs, freqs) (an independent formulation)."""
+    freqs = np.outer(np.asarray(pos, np.float32), inv_freq).astype(np.float32)
+    emb = np.concatenate([freqs, freqs], axis=-1).astype(np.float64)
+    cos, sin = np.cos(emb)[:, None, :], np.sin(emb)[:, None, :]
+    d = x.shape[-1]
+    rot = np.concatenate([-x[..., d // 2:], x[..., : d // 2]], axis=-1)
+    return x * cos + rot * sin
+
+
+def _complex_interleaved(x, pos, inv_freq):
+    """The original Llama form: consecutive pairs as complex numbers times
+    e^(i * angle)."""
+    ang = np.outer(np.asarray(pos, np.float32), inv_freq).astype(np.float32).astype(np.float64)
+    z = x[..., 0::2] + 1j * x[..., 1::2]
+    z = z * np.exp(1j * ang)[:, None, :]
+    out = np.empty_like(x)
+    out[..., 0::2], out[..., 1::2] = z.real, z.imag
+    return out
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_rope_matches_both_published_forms(d):
+    rng = np.random.default_rng(d)
+    x = rng.standard_normal((9, 3, d))
+    pos = np.array([0, 1, 2, 17, 100, 511, 4095, 30000, 131071])
+    inv = (1.0 / (np.float32(10000.0) ** (np.arange(0, d, 2, dtype=np.float32) / d))).astype(np.float32)
+    np.testing.assert_allclose(ref.rope(x, pos, inv, False), _hf_rotate_half(x, pos, inv),
+                               rtol=0, atol=1e-12)
+    np.testing.assert_allclose(ref.rope(x, pos, inv, True), _complex_interleaved(x, pos, inv),
+                               rtol=0, atol=1e-12)
+
+
+def test_rope_closed_forms():
+    rng = np.random.default_rng(3)
+    d = 128
+    x = rng.standard_normal((5, 2, d))
+    inv = (2.0 ** -np.arange(d // 2, dtype=np.float64) / 4).astype(np.float32)  # exact fp32 angles
+    for il in (False, True):
+        # position 0 is the identity
+        np.testing.assert_array_equal(ref.rope(x, np.zeros(5, np.int64), inv, il), x)
+        # each pair keeps its norm
+        y = ref.rope(x, np.arange(5) * 37, inv, il)
+        pa = (x[..., 0::2], x[..., 1::2]) if il else (x[..., : d // 2], x[..., d // 2:])
+        pb = (y[..., 0::2], y[..., 1::2]) if il else (y[..., : d // 2], y[..., d // 2:])
+        np.testing.assert_allclose(pa[0] ** 2 + pa[1] ** 2, pb[0] ** 2 + pb[1] ** 2, atol=1e-12)
+        # scores depend on the position difference only
+        q, k = x[:1], x[1:2]
+        s1 = np.sum(ref.rope(q, np.array([900]), inv, il) * ref.rope(k, np.array([700]), inv, il))
+        s2 = np.sum(ref.rope(q, np.array([200]), inv, il) * ref.rope(k, np.array([0]), inv, il))
+        assert abs(s1 - s2) < 1e-9
+    # interleaved = half-split on de-interleaved dims
+    perm = np.concatenate([np.arange(0, d, 2), np.arange(1, d, 2)])
+    yh = ref.rope(x[..., perm], np.arange(5) * 11, inv, False)
+    yi = ref.rope(x, np.arange(5) * 11, inv, True)
+    np.testing.assert_allclose(yi[..., perm], yh, atol=1e-12)
+
+
+def test_rope_append_positions_and_pages():
+    rng = np.random.default_rng(4)
+    ps, npg, hkv, hq, d = 16, 24, 2, 4, 64
+    q_lens = np.array([3, 1, 20])
+    kv = np.array([3, 40, 25], dtype=np.int64)   # prefixes 0, 39, 5
+    need = (kv + ps - 1) // ps
+    indptr = np.concatenate([[0], np.cumsum(need)])
+    indices = rng.permutation(npg)[: indptr[-1]]
+    q_indptr = np.concatenate([[0], np.cumsum(q_lens)])
+    T = int(q_indptr[-1])
+    pos = ref.token_positions(kv, q_indptr)
+    assert pos.tolist() == [0, 1, 2, 39] + list(range(5, 25))
+    q = rng.standard_normal((T, hq, d)).astype(np.float16)
+    kn = rng.standard_normal((T, hkv, d)).astype(np.float16)
+    vn = rng.standard_normal((T, hkv, d)).astype(np.float16)
+    k_pool = np.zeros((npg, 1, hkv, ps, d), np.float16)
+    v_pool = np.zeros_like(k_pool)
+    inv = (1.0 / (np.float32(10000.0) ** (np.arange(0, d, 2, dtype=np.float32) / d))).astype(np.float32)
+    qr = ref.rope_append_kv(k_pool, v_pool, 0, indptr, indices, kv, q_indptr, q, kn, vn, inv, False)
+    np.testing.assert_array_equal(qr, ref.rope(q, pos, inv, False).astype(np.float16))
+    kr = ref.rope(kn, pos, inv, False).astype(np.float16)
+    for t in range(T):
+        b = int(np.searchsorted(q_indptr, t, side="right") - 1)
+        page = indices[indptr[b] + pos[t] // ps]
+        np.testing.assert_array_equal(k_pool[page, 0, :, pos[t] % ps], kr[t])
+        np.testing.assert_array_equal(v_pool[page, 0, :, pos[t] % ps], vn[t])
