@@ -19,7 +19,8 @@
  *   - All device work is enqueued on the given stream; no function
  *     synchronises the device or the stream, and no function allocates
  *     device memory: scratch space is passed in by the caller.
- *   - KV data is fp16. Element (page, layer, kv_head, slot, dim) of the K (or
+ *   - KV data is fp16 or bf16 (kunserve_kv_pool.dtype; q, outputs and new
+ *     K/V share it). Element (page, layer, kv_head, slot, dim) of the K (or
  *     V) pool lives at
  *        page*page_stride + layer*layer_stride + kv_head*head_stride
  *        + slot*token_stride + dim                      (in elements)
@@ -50,10 +51,16 @@ enum {
   KUNSERVE_EHIP = -5        /* a HIP runtime call failed                     */
 };
 
+/* Element types of pools and activations. */
+enum {
+  KUNSERVE_DTYPE_F16 = 0,
+  KUNSERVE_DTYPE_BF16 = 1
+};
+
 /* Paged KV pool (separate K and V pools with identical strides). */
 typedef struct {
-  void* k;                 /* device, fp16 */
-  void* v;                 /* device, fp16 */
+  void* k;                 /* device, 16-bit elements of type dtype */
+  void* v;
   int64_t num_pages;       /* page ids must lie in [0, num_pages)            */
   int64_t page_stride;     /* elements between consecutive pages             */
   int64_t layer_stride;
@@ -63,6 +70,7 @@ typedef struct {
   int32_t num_kv_heads;
   int32_t page_size;       /* tokens per page; power of two, >= 4            */
   int32_t head_dim;        /* 64, 128 or 256                                 */
+  int32_t dtype;           /* KUNSERVE_DTYPE_*: pool, q, out, new K/V alike   */
 } kunserve_kv_pool;
 
 /* Per-step page table in CSR form, device resident. */
@@ -73,10 +81,10 @@ typedef struct {
   int32_t num_seqs;
 } kunserve_page_table;
 
-/* Strided fp16 activation tensor [num_tokens, num_heads, head_dim]
- * (head_dim contiguous). */
+/* Strided activation tensor [num_tokens, num_heads, head_dim] (head_dim
+ * contiguous), of the pool's dtype. */
 typedef struct {
-  void* data;              /* device, fp16 */
+  void* data;              /* device */
   int64_t token_stride;    /* elements */
   int64_t head_stride;     /* elements */
 } kunserve_tensor3;
@@ -103,7 +111,7 @@ int kunserve_copy_blocks(const kunserve_kv_pool* pool,
 /* kv_exchange phase 1 "pack" (kunserve/flash_backend.py:930-985): gather
  * layers [layer_begin, layer_end) of pages page_ids[0..n) into a contiguous
  * scratch buffer laid out [layer_end-layer_begin][n][2 (K,V)][num_kv_heads]
- * [page_size][head_dim] (fp16, densely packed). */
+ * [page_size][head_dim] (16-bit elements, densely packed). */
 int kunserve_kv_pack(const kunserve_kv_pool* pool, int32_t layer_begin,
                      int32_t layer_end, const int32_t* page_ids_dev, int64_t n,
                      void* scratch_dev, int64_t scratch_bytes,
@@ -204,7 +212,8 @@ int64_t kunserve_decode_workspace_bytes(const kunserve_decode_plan_info* info,
 /* o[b, h, :] = softmax(q[b, h, :] . K[b, g(h)]^T * sm_scale) . V[b, g(h)]
  * over the kv_len[b] tokens of sequence b in layer `layer`, with
  * g(h) = h / (num_qo_heads / num_kv_heads). q and out are
- * [num_seqs, num_qo_heads, head_dim] fp16; fp32 accumulation. */
+ * [num_seqs, num_qo_heads, head_dim] of the pool dtype (fp16 or bf16);
+ * fp32 accumulation. */
 int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer,
                           const kunserve_page_table* table,
                           const kunserve_tensor3* q, kunserve_tensor3* out,
@@ -255,8 +264,9 @@ int64_t kunserve_prefill_workspace_bytes(const kunserve_prefill_plan_info* info)
 /* Causal attention of the q_len[b] new rows of each sequence against its
  * kv_len[b] cached tokens (new ones already appended): q row i of
  * sequence b sees positions [0, kv_len[b] - q_len[b] + i]. q and out are
- * [num_tokens, num_qo_heads, head_dim] fp16 with rows grouped by q_indptr.
- * fp16 MFMA for Q.K^T and P.V, fp32 accumulation and softmax. */
+ * [num_tokens, num_qo_heads, head_dim] of the pool dtype with rows grouped
+ * by q_indptr. fp16 or bf16 MFMA for Q.K^T and P.V, fp32 accumulation and
+ * softmax. */
 int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
                            const kunserve_page_table* table,
                            const int32_t* q_indptr_dev,

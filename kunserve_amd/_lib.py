@@ -28,8 +28,12 @@ class KVPool(Structure):
         ("num_pages", c_int64), ("page_stride", c_int64), ("layer_stride", c_int64),
         ("head_stride", c_int64), ("token_stride", c_int64),
         ("num_layers", c_int32), ("num_kv_heads", c_int32),
-        ("page_size", c_int32), ("head_dim", c_int32),
+        ("page_size", c_int32), ("head_dim", c_int32), ("dtype", c_int32),
     ]
+
+
+DTYPE_F16 = 0    # KUNSERVE_DTYPE_F16
+DTYPE_BF16 = 1   # KUNSERVE_DTYPE_BF16
 
 
 class PageTable(Structure):

@@ -28,6 +28,8 @@ int check_pool(const kunserve_kv_pool* p, bool need_vec_align) {
                 "page_size %d must be a power of two >= 4", p->page_size);
   KSV_CHECK_ARG(p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256,
                 "head_dim %d not in {64, 128, 256}", p->head_dim);
+  KSV_CHECK_ARG(p->dtype == KUNSERVE_DTYPE_F16 || p->dtype == KUNSERVE_DTYPE_BF16,
+                "dtype %d is neither KUNSERVE_DTYPE_F16 nor KUNSERVE_DTYPE_BF16", p->dtype);
   KSV_CHECK_ARG(p->page_stride > 0 && p->layer_stride >= 0 && p->head_stride >= 0 &&
                     p->token_stride >= p->head_dim,
                 "bad pool strides");

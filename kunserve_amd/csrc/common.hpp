@@ -18,6 +18,10 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));  // fdot2 operand
+typedef __bf16 bf16;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -132,6 +136,45 @@ __device__ __forceinline__ float dot8(f16x8 a, f16x8 b, float acc) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2(pa[i], pb[i], acc, false);
   return acc;
+}
+// The same for bf16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot8(bf16x8 a, bf16x8 b, float acc) {
+  const bf16x2* pa = reinterpret_cast<const bf16x2*>(&a);
+  const bf16x2* pb = reinterpret_cast<const bf16x2*>(&b);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2_f32_bf16(pa[i], pb[i], acc, false);
+  return acc;
+}
+
+// ------------------------------------------------ element-type generics
+// The attention kernels are templates over the 16-bit element type T (f16
+// or bf16). Pools, q and outputs are addressed as 16-bit storage; these
+// helpers give the typed vector view and the matching MFMA.
+template <typename T> struct Vec;
+template <> struct Vec<f16> { typedef f16x8 v8; typedef f16x4 v4; };
+template <> struct Vec<bf16> { typedef bf16x8 v8; typedef bf16x4 v4; };
+
+template <typename T>
+__device__ __forceinline__ typename Vec<T>::v8 load_v8(const void* p) {
+  return *reinterpret_cast<const typename Vec<T>::v8*>(p);
+}
+template <typename T>
+__device__ __forceinline__ typename Vec<T>::v8 load_v8_nt(const void* p) {
+  return __builtin_bit_cast(typename Vec<T>::v8,
+                            __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+}
+
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 }  // namespace kunserve

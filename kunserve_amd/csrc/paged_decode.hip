@@ -13,7 +13,8 @@
 //    that each K/V access is one 16-byte load per lane. A wave reads 1 KiB
 //    of K and 1 KiB of V per load instruction (4 tokens x 256 B for
 //    head_dim 128), four of each in flight per 16-token chunk.
-//  * Q.K uses v_dot2_f32_f16 and a DPP butterfly inside each 16-lane row;
+//  * fp16 and bf16 pools (kernels are templates over the element type).
+//  * Q.K uses v_dot2_f32_f16 / _bf16 and a DPP butterfly inside each 16-lane row;
 //    the softmax is an online (running max) softmax in fp32 kept per row,
 //    merged across rows with shuffles and across waves through LDS.
 //  * Sequences longer than one partition write fp32 partial results with
@@ -60,8 +61,9 @@ struct DecodeArgs {
   float scale_log2;         // sm_scale * log2(e)
 };
 
-template <int D, int G>
+template <typename T, int D, int G>
 __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
+  typedef typename Vec<T>::v8 V8;
   constexpr int LPT = D / 8;            // lanes per token row (16 for D = 128)
   constexpr int TPL = kWave / LPT;      // tokens per load instruction (4)
   constexpr int CHUNK = TPL * kLoadsPerChunk;  // tokens per wave iteration (16)
@@ -92,10 +94,10 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
     s_pages[i] = (p >= 0 && p < a.num_pages) ? p : -1;
   }
 
-  f16x8 qv[G];
+  V8 qv[G];
 #pragma unroll
   for (int g = 0; g < G; ++g)
-    qv[g] = load_f16x8(a.q + int64_t(seq) * a.q_tok + int64_t(hq0 + g) * a.q_head + col * 8);
+    qv[g] = load_v8<T>(a.q + int64_t(seq) * a.q_tok + int64_t(hq0 + g) * a.q_head + col * 8);
 
   float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -115,7 +117,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
   // non-temporal: every K/V byte is read once, so it should not displace
   // the page table and q in the caches.
   struct Chunk {
-    f16x8 k[kLoadsPerChunk], v[kLoadsPerChunk];
+    V8 k[kLoadsPerChunk], v[kLoadsPerChunk];
     bool ok[kLoadsPerChunk];
   };
   // Loads are issued unconditionally (lanes past the partition read the
@@ -131,8 +133,8 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
       const int p = (c < nchunks && t < te) ? s_pages[pi] : -1;
       ch.ok[i] = p >= 0;
       const int64_t off = int64_t(max(p, 0)) * a.page_stride + int64_t(t & page_mask) * a.token_stride;
-      ch.k[i] = load_f16x8_nt(ch.ok[i] ? kb + off : g_zero_row + col * 8);
-      ch.v[i] = load_f16x8_nt(ch.ok[i] ? vb + off : g_zero_row + col * 8);
+      ch.k[i] = load_v8_nt<T>(ch.ok[i] ? kb + off : g_zero_row + col * 8);
+      ch.v[i] = load_v8_nt<T>(ch.ok[i] ? vb + off : g_zero_row + col * 8);
     }
   };
   auto consume = [&](const Chunk& ch) {
@@ -236,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
     const float r = lsum > 0.f ? o / lsum : 0.f;
     const int hq = hq0 + g;
     if (slot < 0) {
-      a.out[int64_t(seq) * a.o_tok + int64_t(hq) * a.o_head + d] = f16(r);
+      reinterpret_cast<T*>(a.out)[int64_t(seq) * a.o_tok + int64_t(hq) * a.o_head + d] = T(r);
     } else {
       a.part_o[(int64_t(slot) * a.num_qo_heads + hq) * D + d] = r;
       if (d == 0)
@@ -265,9 +267,10 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
 //    each 16-token half, and the V gather uses the same token order.
 //  * Online softmax per head column in fp32 with a lazy running max, merged
 //    across waves through LDS; partial results as in the VALU kernel.
-template <int G>
+template <typename T, int G>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_mfma_kernel(DecodeArgs a) {
+  typedef typename Vec<T>::v8 V8;
   constexpr int D = 128;
   constexpr int STEP = 32;                  // tokens per wave iteration
   constexpr int LOADS = STEP / 4;           // 16-byte loads per lane per step (K and V each)
@@ -275,7 +278,7 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   static_assert(G <= 16, "one 16-column MFMA tile of query heads");
 
   __shared__ int s_pages[kMaxPartPages];
-  __shared__ __attribute__((aligned(16))) f16 s_kv[kWaves * BLK];   // 32 KiB: K, then V
+  __shared__ __attribute__((aligned(16))) T s_kv[kWaves * BLK];   // 32 KiB: K, then V
   __shared__ float s_m[kWaves][G];
   __shared__ float s_l[kWaves][G];
 
@@ -302,12 +305,12 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   }
 
   // Q^T as the B operand: dim step s covers dims 32s + 8tg .. +8 of head j.
-  f16x8 qb[4];
+  V8 qb[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s)
-    qb[s] = j < G ? load_f16x8(a.q + int64_t(seq) * a.q_tok + int64_t(hq0 + j) * a.q_head +
+    qb[s] = j < G ? load_v8<T>(a.q + int64_t(seq) * a.q_tok + int64_t(hq0 + j) * a.q_head +
                                32 * s + 8 * tg)
-                  : f16x8{};
+                  : V8{};
   f32x4 o[8];
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) o[mt] = f32x4{};
@@ -318,13 +321,13 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   const f16* kb = a.k + int64_t(hkv) * a.head_stride + lcol * 8;
   const f16* vb = a.v + int64_t(hkv) * a.head_stride + lcol * 8;
   const int nsteps = (te - tb + STEP - 1) / STEP;
-  f16* sk = s_kv + wave * BLK;   // holds the step's K rows, then its V rows
-  f16* sv = sk;
+  T* sk = s_kv + wave * BLK;   // holds the step's K rows, then its V rows
+  T* sv = sk;
   // Element (token t, dim d) of a block: t*128 + (((d >> 3) ^ (t & 15)) << 3) + (d & 7).
   auto blk_off = [](int t, int chunk) { return t * D + ((chunk ^ (t & 15)) << 3); };
 
   struct Step {
-    f16x8 k[LOADS], v[LOADS];
+    V8 k[LOADS], v[LOADS];
   };
   // Unconditional loads (see the VALU kernel): past-the-end lanes and bad
   // page ids read the zero row.
@@ -336,14 +339,14 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
       const int p = (c < nsteps && t < te) ? s_pages[pi] : -1;
       const bool ok = p >= 0;
       const int64_t off = int64_t(max(p, 0)) * a.page_stride + int64_t(t & page_mask) * a.token_stride;
-      st.k[i] = load_f16x8_nt(ok ? kb + off : g_zero_row + lcol * 8);
-      st.v[i] = load_f16x8_nt(ok ? vb + off : g_zero_row + lcol * 8);
+      st.k[i] = load_v8_nt<T>(ok ? kb + off : g_zero_row + lcol * 8);
+      st.v[i] = load_v8_nt<T>(ok ? vb + off : g_zero_row + lcol * 8);
     }
   };
-  auto stash = [&](const f16x8 (&rows)[LOADS]) {
+  auto stash = [&](const V8 (&rows)[LOADS]) {
 #pragma unroll
     for (int i = 0; i < LOADS; ++i)
-      *reinterpret_cast<f16x8*>(&sk[blk_off(4 * i + lrow, lcol)]) = rows[i];
+      *reinterpret_cast<V8*>(&sk[blk_off(4 * i + lrow, lcol)]) = rows[i];
   };
   // Scores of the step whose K rows are in the block.
   auto scores = [&](f32x4 (&sc)[2]) {
@@ -355,8 +358,8 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
       sc[sub] = f32x4{};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const f16x8 ka = *reinterpret_cast<const f16x8*>(&sk[blk_off(t, 4 * s + tg)]);
-        sc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sc[sub], 0, 0, 0);
+        const V8 ka = *reinterpret_cast<const V8*>(&sk[blk_off(t, 4 * s + tg)]);
+        sc[sub] = mfma16(ka, qb[s], sc[sub]);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -383,27 +386,27 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) o[mt] *= alpha;
     }
-    f16x8 pb;
+    V8 pb;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float p = fast_exp2(fmaf(sc[sub][v], a.scale_log2, -m));
         lsum += p;
-        pb[sub * 4 + v] = f16(p);
+        pb[sub * 4 + v] = T(p);
       }
     __builtin_amdgcn_wave_barrier();
     // O^T: A operand = V[token 16 sub + 4 tg + v][dim 16 mt + j] for e = 4 sub + v.
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       const int d = 16 * mt + j;
-      f16x8 va;
+      V8 va;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int t = 16 * (e >> 2) + 4 * tg + (e & 3);
         va[e] = sv[blk_off(t, d >> 3) + (d & 7)];
       }
-      o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[mt], 0, 0, 0);
+      o[mt] = mfma16(va, pb, o[mt]);
     }
     __builtin_amdgcn_wave_barrier();
   };
@@ -456,7 +459,7 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
     const float r = ls > 0.f ? acc / ls : 0.f;
     const int hq = hq0 + g;
     if (slot < 0) {
-      a.out[int64_t(seq) * a.o_tok + int64_t(hq) * a.o_head + d] = f16(r);
+      reinterpret_cast<T*>(a.out)[int64_t(seq) * a.o_tok + int64_t(hq) * a.o_head + d] = T(r);
     } else {
       a.part_o[(int64_t(slot) * a.num_qo_heads + hq) * D + d] = r;
       if (d == 0)
@@ -469,10 +472,10 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
 // q head). Lane j first reads the log-sum-exp of partition j, so the
 // weights come from one round of loads; each lane then accumulates D/64
 // dimensions over the partitions.
-template <int D>
+template <typename T, int D>
 __global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merges,
                                                              const float* part_o,
-                                                             const float* part_lse, f16* out,
+                                                             const float* part_lse, T* out,
                                                              int64_t o_tok, int64_t o_head,
                                                              int32_t num_qo_heads) {
   constexpr int DPL = D / kWave;
@@ -507,9 +510,9 @@ __global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merg
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) wsum += __shfl_xor(wsum, off);
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  f16* dst = out + int64_t(seq) * o_tok + int64_t(hq) * o_head + lane * DPL;
+  T* dst = out + int64_t(seq) * o_tok + int64_t(hq) * o_head + lane * DPL;
 #pragma unroll
-  for (int e = 0; e < DPL; ++e) dst[e] = f16(o[e] * inv);
+  for (int e = 0; e < DPL; ++e) dst[e] = T(o[e] * inv);
 }
 
 int pick_group(int ratio) {
@@ -519,7 +522,7 @@ int pick_group(int ratio) {
   return 1;
 }
 
-template <int D>
+template <typename T, int D>
 int launch_decode(const DecodeArgs& a, int group, dim3 grid, hipStream_t s) {
   // Groups of 4 and 8 query heads per KV head run on MFMA (Llama-3-8B shape:
   // 6.05 TB/s vs 5.23 TB/s on VALU); for 1 and 2 the VALU kernel is as fast
@@ -527,31 +530,58 @@ int launch_decode(const DecodeArgs& a, int group, dim3 grid, hipStream_t s) {
   if constexpr (D == 128) {
     if (group == 4 || group == 8) {
       if (group == 4)
-        paged_decode_mfma_kernel<4><<<grid, kThreads, 0, s>>>(a);
+        paged_decode_mfma_kernel<T, 4><<<grid, kThreads, 0, s>>>(a);
       else
-        paged_decode_mfma_kernel<8><<<grid, kThreads, 0, s>>>(a);
+        paged_decode_mfma_kernel<T, 8><<<grid, kThreads, 0, s>>>(a);
       KSV_CHECK_LAUNCH();
       return KUNSERVE_OK;
     }
   }
   switch (group) {
-    case 1: paged_decode_kernel<D, 1><<<grid, kThreads, 0, s>>>(a); break;
-    case 2: paged_decode_kernel<D, 2><<<grid, kThreads, 0, s>>>(a); break;
-    case 4: paged_decode_kernel<D, 4><<<grid, kThreads, 0, s>>>(a); break;
-    case 8: paged_decode_kernel<D, 8><<<grid, kThreads, 0, s>>>(a); break;
+    case 1: paged_decode_kernel<T, D, 1><<<grid, kThreads, 0, s>>>(a); break;
+    case 2: paged_decode_kernel<T, D, 2><<<grid, kThreads, 0, s>>>(a); break;
+    case 4: paged_decode_kernel<T, D, 4><<<grid, kThreads, 0, s>>>(a); break;
+    case 8: paged_decode_kernel<T, D, 8><<<grid, kThreads, 0, s>>>(a); break;
     default: set_error("unsupported group size %d", group); return KUNSERVE_EUNSUPPORTED;
   }
   KSV_CHECK_LAUNCH();
   return KUNSERVE_OK;
 }
 
-template <int D>
+template <typename T, int D>
 int launch_merge(const int32_t* merges, int num_merge, const float* po, const float* pl, f16* out,
                  int64_t o_tok, int64_t o_head, int hq, hipStream_t s) {
   dim3 grid(num_merge, hq);
-  decode_merge_kernel<D><<<grid, kWave, 0, s>>>(merges, po, pl, out, o_tok, o_head, hq);
+  decode_merge_kernel<T, D><<<grid, kWave, 0, s>>>(merges, po, pl, reinterpret_cast<T*>(out),
+                                                   o_tok, o_head, hq);
   KSV_CHECK_LAUNCH();
   return KUNSERVE_OK;
+}
+
+// Partition kernel, then (for split rows) the merge, for element type T.
+template <typename T>
+int run_decode(const DecodeArgs& a, const kunserve_decode_plan_info& info, const int32_t* plan_dev,
+               int head_dim, int num_qo_heads, dim3 grid, hipStream_t s) {
+  int rc;
+  switch (head_dim) {
+    case 64: rc = launch_decode<T, 64>(a, info.group_size, grid, s); break;
+    case 128: rc = launch_decode<T, 128>(a, info.group_size, grid, s); break;
+    case 256: rc = launch_decode<T, 256>(a, info.group_size, grid, s); break;
+    default: set_error("head_dim %d not compiled", head_dim); return KUNSERVE_EUNSUPPORTED;
+  }
+  if (rc || info.num_merge == 0) return rc;
+  const int32_t* merges = plan_dev + 4 * int64_t(info.num_work);
+  switch (head_dim) {
+    case 64:
+      return launch_merge<T, 64>(merges, info.num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
+                                 a.o_head, num_qo_heads, s);
+    case 128:
+      return launch_merge<T, 128>(merges, info.num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
+                                  a.o_head, num_qo_heads, s);
+    default:
+      return launch_merge<T, 256>(merges, info.num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
+                                  a.o_head, num_qo_heads, s);
+  }
 }
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -705,23 +735,7 @@ extern "C" int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   dim3 grid(info->num_work, num_qo_heads / info->group_size);
-  switch (pool->head_dim) {
-    case 64: rc = launch_decode<64>(a, info->group_size, grid, s); break;
-    case 128: rc = launch_decode<128>(a, info->group_size, grid, s); break;
-    case 256: rc = launch_decode<256>(a, info->group_size, grid, s); break;
-    default: set_error("head_dim %d not compiled", pool->head_dim); return KUNSERVE_EUNSUPPORTED;
-  }
-  if (rc || info->num_merge == 0) return rc;
-  const int32_t* merges = plan_dev + 4 * int64_t(info->num_work);
-  switch (pool->head_dim) {
-    case 64:
-      return launch_merge<64>(merges, info->num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
-                              a.o_head, num_qo_heads, s);
-    case 128:
-      return launch_merge<128>(merges, info->num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
-                               a.o_head, num_qo_heads, s);
-    default:
-      return launch_merge<256>(merges, info->num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
-                               a.o_head, num_qo_heads, s);
-  }
+  if (pool->dtype == KUNSERVE_DTYPE_BF16)
+    return run_decode<bf16>(a, *info, plan_dev, pool->head_dim, num_qo_heads, grid, s);
+  return run_decode<f16>(a, *info, plan_dev, pool->head_dim, num_qo_heads, grid, s);
 }

@@ -4,8 +4,9 @@
 //
 // Append: HBM-bound scatter of the new tokens' K/V rows into their pages.
 //
-// Attention: flash-attention style on fp16 MFMA (v_mfma_f32_32x32x16_f16,
-// gfx950), fp32 accumulation and online softmax.
+// Attention: flash-attention style on fp16 or bf16 MFMA
+// (v_mfma_f32_32x32x16_f16 / _bf16, gfx950), fp32 accumulation and online
+// softmax; kernels are templates over the element type.
 //  * Workgroup = 8 waves = 256 query rows of one (sequence, q head); each
 //    wave owns 32 rows. Two waves share a SIMD (waves w and w + 4).
 //  * K/V tiles of 64 tokens are gathered from pages into double-buffered
@@ -87,10 +88,11 @@ constexpr int kVHalves = kTileKV * kVPitch;
 // lanes 4k..4k+3 addressing 4 consecutive dims of token t_k, lane i gets
 // V[t_k][dbase + i] for k = 0..3: four tokens of its own dim.
 typedef short i16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ f16x4 lds_read_tr16(const f16* p) {
+template <typename T>
+__device__ __forceinline__ typename Vec<T>::v4 lds_read_tr16(const T* p) {
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
   const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-  return __builtin_bit_cast(f16x4, r);
+  return __builtin_bit_cast(typename Vec<T>::v4, r);
 }
 
 // Page ids a workgroup stages in LDS (rows up to 32768 tokens at page 16).
@@ -104,11 +106,13 @@ __device__ __attribute__((aligned(16))) f16 g_zero_row[kD];
 // issue only K/V loads; waiting for an older tile's data then leaves the
 // newer tile's loads in flight. Rows with more pages than fit use the
 // global-lookup variant (same results).
-template <bool STAGED>
+template <typename T, bool STAGED>
 __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) {
+  typedef typename Vec<T>::v8 V8;
+  typedef typename Vec<T>::v4 V4;
   __shared__ int s_pg[STAGED ? kMaxStagedPages : 1];
-  __shared__ __attribute__((aligned(16))) f16 sK[2 * kKHalves];
-  __shared__ __attribute__((aligned(16))) f16 sV[2 * kVHalves];
+  __shared__ __attribute__((aligned(16))) T sK[2 * kKHalves];
+  __shared__ __attribute__((aligned(16))) T sV[2 * kVHalves];
 
   const int32_t* item = a.tiles + kRec * blockIdx.x;
   const int seq = item[0];
@@ -152,11 +156,11 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   }
 
   // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
-  f16x8 qf[8];
+  V8 qf[8];
   {
     const f16* qp = a.q + int64_t(qb + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = row_ok ? load_f16x8(qp + 16 * s + 8 * h) : f16x8{};
+    for (int s = 0; s < 8; ++s) qf[s] = row_ok ? load_v8<T>(qp + 16 * s + 8 * h) : V8{};
   }
 
   f32x16 o[4];
@@ -177,7 +181,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   const int ld_t = tid >> 4;
   const int ld_c = (tid & 15) * 8;
   struct Regs {
-    f16x8 k[kLoadsPerThread], v[kLoadsPerThread];
+    V8 k[kLoadsPerThread], v[kLoadsPerThread];
   };
   int pid[kLoadsPerThread];
   auto read_ids = [&](int n0) {
@@ -199,16 +203,16 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
                            (uint32_t(tok & page_mask) * a.token_stride + ld_c);
       // Past-the-end tokens and bad ids read the zero row (cache-resident).
       const bool ok = pid[i] >= 0;
-      rg.k[i] = load_f16x8(ok ? kbase + off : g_zero_row + ld_c);
-      rg.v[i] = load_f16x8(ok ? vbase + off : g_zero_row + ld_c);
+      rg.k[i] = load_v8<T>(ok ? kbase + off : g_zero_row + ld_c);
+      rg.v[i] = load_v8<T>(ok ? vbase + off : g_zero_row + ld_c);
     }
   };
   auto stash = [&](int buf, const Regs& rg) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
       const int t = ld_t + kRowsPerLoad * i;
-      *reinterpret_cast<f16x8*>(&sK[buf * kKHalves + t * kKPitch + ld_c]) = rg.k[i];
-      *reinterpret_cast<f16x8*>(&sV[buf * kVHalves + t * kVPitch + ld_c]) = rg.v[i];
+      *reinterpret_cast<V8*>(&sK[buf * kKHalves + t * kKPitch + ld_c]) = rg.k[i];
+      *reinterpret_cast<V8*>(&sV[buf * kVHalves + t * kVPitch + ld_c]) = rg.v[i];
     }
   };
 
@@ -222,18 +226,17 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   const int vb0 = (4 * (g16 >> 1) + (i16 >> 2)) * kVPitch + 16 * (g16 & 1) + 4 * (i16 & 3);
 
   auto compute = [&](int buf, int n0) {
-    const f16* kt = sK + buf * kKHalves + kb0;
-    const f16* vt = sV + buf * kVHalves + vb0;
+    const T* kt = sK + buf * kKHalves + kb0;
+    const T* vt = sV + buf * kVHalves + vb0;
     // S^T tiles: rows = kv tokens 32*mt + i, columns = query rows.
     f32x16 st[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-          *reinterpret_cast<const f16x8*>(kt + 32 * mt * kKPitch), qf[0], f32x16{}, 0, 0, 0);
+      st[mt] = mfma32(*reinterpret_cast<const V8*>(kt + 32 * mt * kKPitch), qf[0], f32x16{});
 #pragma unroll
       for (int s = 1; s < 8; ++s) {
-        const f16x8 ka = *reinterpret_cast<const f16x8*>(kt + 32 * mt * kKPitch + 16 * s);
-        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[s], st[mt], 0, 0, 0);
+        const V8 ka = *reinterpret_cast<const V8*>(kt + 32 * mt * kKPitch + 16 * s);
+        st[mt] = mfma32(ka, qf[s], st[mt]);
       }
     }
     // Lane holds tokens n0 + 32mt + 8(v/4) + 4h + v%4 of query row r.
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
 
     // P^T as B operands: k-step ks covers tokens 16ks + 4h + {0..3} and
     // 16ks + 8 + 4h + {0..3}, i.e. accumulator entries v = 8(ks%2) + e of tile ks/2.
-    f16x8 pb[4];
+    V8 pb[4];
     float ps = 0.f;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -276,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
       for (int v = 0; v < 16; ++v) {
         const float p = fast_exp2(fmaf(st[mt][v], a.scale_log2, -m));
         ps += p;
-        pb[2 * mt + (v >> 3)][v & 7] = f16(p);
+        pb[2 * mt + (v >> 3)][v & 7] = T(p);
       }
     lsum += ps;
 
@@ -286,10 +289,10 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const f16x4 lo = lds_read_tr16(vt + 16 * ks * kVPitch + 32 * dt);
-        const f16x4 hi = lds_read_tr16(vt + (16 * ks + 8) * kVPitch + 32 * dt);
-        const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[ks], o[dt], 0, 0, 0);
+        const V4 lo = lds_read_tr16(vt + 16 * ks * kVPitch + 32 * dt);
+        const V4 hi = lds_read_tr16(vt + (16 * ks + 8) * kVPitch + 32 * dt);
+        const V8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[dt] = mfma32(va, pb[ks], o[dt]);
       }
     }
   };
@@ -336,9 +339,9 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const f16x4 val = {f16(o[dt][4 * g] * inv), f16(o[dt][4 * g + 1] * inv),
-                           f16(o[dt][4 * g + 2] * inv), f16(o[dt][4 * g + 3] * inv)};
-        *reinterpret_cast<f16x4*>(op + 32 * dt + 8 * g + 4 * h) = val;
+        const V4 val = {T(o[dt][4 * g] * inv), T(o[dt][4 * g + 1] * inv),
+                        T(o[dt][4 * g + 2] * inv), T(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<V4*>(op + 32 * dt + 8 * g + 4 * h) = val;
       }
     return;
   }
@@ -374,7 +377,9 @@ struct MergeArgs {
 // Grid (merge record, block of kMergeRows rows); one thread per (row, 8 dims).
 constexpr int kMergeRows = 256 / (kD / 8);
 
+template <typename T>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(MergeArgs a) {
+  typedef typename Vec<T>::v4 V4;
   const int32_t* rec = a.merges + kMergeRec * blockIdx.x;
   const int seq = rec[0], q0 = rec[1], hq = rec[2], s0 = rec[3], n = rec[4];
   const int qb = a.q_indptr[seq];
@@ -405,10 +410,10 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MergeArgs a) {
     }
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
     f16* op = a.out + int64_t(qb + q0 + row) * a.o_tok + int64_t(hq) * a.o_head + 8 * c;
-    *reinterpret_cast<f16x4*>(op) = {f16(acc[0] * inv), f16(acc[1] * inv), f16(acc[2] * inv),
-                                     f16(acc[3] * inv)};
-    *reinterpret_cast<f16x4*>(op + 4) = {f16(acc[4] * inv), f16(acc[5] * inv), f16(acc[6] * inv),
-                                         f16(acc[7] * inv)};
+    *reinterpret_cast<V4*>(op) = {T(acc[0] * inv), T(acc[1] * inv), T(acc[2] * inv),
+                                  T(acc[3] * inv)};
+    *reinterpret_cast<V4*>(op + 4) = {T(acc[4] * inv), T(acc[5] * inv), T(acc[6] * inv),
+                                      T(acc[7] * inv)};
   }
 }
 
@@ -498,7 +503,9 @@ __device__ __forceinline__ void rope_pair(float& a, float& b, float c, float s) 
   b = fmaf(y, c, x * s);
 }
 
+template <typename T>
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
+  typedef typename Vec<T>::v8 V8;
   const int units = a.head_dim / 16;   // 16-dim units per head
   const int64_t per_tok = int64_t(a.num_qo_heads + a.num_kv_heads) * units;
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -529,7 +536,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
     const float ang = float(pos) * a.inv_freq[f0 + j];
     sincosf(ang, &sn[j], &cs[j]);
   }
-  auto rotate = [&](const f16x8& x0, const f16x8& x1, f16x8& y0, f16x8& y1) {
+  auto rotate = [&](const V8& x0, const V8& x1, V8& y0, V8& y1) {
     float u[16];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -547,17 +554,17 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      y0[e] = f16(u[e]);
-      y1[e] = f16(u[8 + e]);
+      y0[e] = T(u[e]);
+      y1[e] = T(u[8 + e]);
     }
   };
 
   if (slot < a.num_qo_heads) {
     f16* qp = a.q + int64_t(tok) * a.q_tok + int64_t(slot) * a.q_head;
-    f16x8 y0, y1;
-    rotate(load_f16x8(qp + d0), load_f16x8(qp + d1), y0, y1);
-    store_f16x8(qp + d0, y0);
-    store_f16x8(qp + d1, y1);
+    V8 y0, y1;
+    rotate(load_v8<T>(qp + d0), load_v8<T>(qp + d1), y0, y1);
+    *reinterpret_cast<V8*>(qp + d0) = y0;
+    *reinterpret_cast<V8*>(qp + d1) = y1;
     return;
   }
   const int head = slot - a.num_qo_heads;
@@ -567,12 +574,28 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
                       int64_t(pos & ((1 << a.page_shift) - 1)) * a.token_stride;
   const f16* kp = a.k_new + int64_t(tok) * a.k_tok + int64_t(head) * a.k_head;
   const f16* vp = a.v_new + int64_t(tok) * a.v_tok + int64_t(head) * a.v_head;
-  f16x8 y0, y1;
-  rotate(load_f16x8(kp + d0), load_f16x8(kp + d1), y0, y1);
-  store_f16x8(a.k + dst + d0, y0);
-  store_f16x8(a.k + dst + d1, y1);
+  V8 y0, y1;
+  rotate(load_v8<T>(kp + d0), load_v8<T>(kp + d1), y0, y1);
+  *reinterpret_cast<V8*>(a.k + dst + d0) = y0;
+  *reinterpret_cast<V8*>(a.k + dst + d1) = y1;
   store_f16x8(a.v + dst + d0, load_f16x8(vp + d0));
   store_f16x8(a.v + dst + d1, load_f16x8(vp + d1));
+}
+
+// Attention (page ids staged in LDS when they fit), then the split merge.
+template <typename T>
+int run_prefill(const PrefillArgs& a, const MergeArgs& m, int num_tiles, int num_merge,
+                bool staged, hipStream_t s) {
+  if (staged)
+    paged_prefill_kernel<T, true><<<dim3(num_tiles), kThreads, 0, s>>>(a);
+  else
+    paged_prefill_kernel<T, false><<<dim3(num_tiles), kThreads, 0, s>>>(a);
+  KSV_CHECK_LAUNCH();
+  if (num_merge > 0) {
+    prefill_merge_kernel<T><<<dim3(num_merge, kTileQ / kMergeRows), 256, 0, s>>>(m);
+    KSV_CHECK_LAUNCH();
+  }
+  return KUNSERVE_OK;
 }
 
 }  // namespace
@@ -638,7 +661,12 @@ extern "C" int kunserve_rope_append_kv(const kunserve_kv_pool* pool, int32_t lay
       int64_t(num_tokens) * (num_qo_heads + pool->num_kv_heads) * (pool->head_dim / 16);
   const int64_t blocks = (threads + 255) / 256;
   KSV_CHECK_ARG(blocks < (int64_t(1) << 31), "rope append too large for one launch");
-  rope_append_kernel<<<dim3(unsigned(blocks)), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
+  if (pool->dtype == KUNSERVE_DTYPE_BF16)
+    rope_append_kernel<bf16>
+        <<<dim3(unsigned(blocks)), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
+  else
+    rope_append_kernel<f16>
+        <<<dim3(unsigned(blocks)), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
   KSV_CHECK_LAUNCH();
   return KUNSERVE_OK;
 }
@@ -925,25 +953,18 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   a.ratio = num_qo_heads / pool->num_kv_heads;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   const int64_t pages_needed = (int64_t(info->max_kv_len) + pool->page_size - 1) / pool->page_size;
-  if (pages_needed <= kMaxStagedPages)
-    paged_prefill_kernel<true><<<dim3(info->num_tiles), kThreads, 0,
-                                 reinterpret_cast<hipStream_t>(stream)>>>(a);
-  else
-    paged_prefill_kernel<false><<<dim3(info->num_tiles), kThreads, 0,
-                                  reinterpret_cast<hipStream_t>(stream)>>>(a);
-  KSV_CHECK_LAUNCH();
-  if (info->num_merge > 0) {
-    MergeArgs m{};
-    m.merges = plan_dev + int64_t(kRec) * info->num_tiles;
-    m.part_o = a.part_o;
-    m.part_ml = a.part_ml;
-    m.q_indptr = q_indptr_dev;
-    m.out = a.out;
-    m.o_tok = a.o_tok;
-    m.o_head = a.o_head;
-    prefill_merge_kernel<<<dim3(info->num_merge, kTileQ / kMergeRows), 256, 0,
-                           reinterpret_cast<hipStream_t>(stream)>>>(m);
-    KSV_CHECK_LAUNCH();
-  }
-  return KUNSERVE_OK;
+  MergeArgs m{};
+  m.merges = plan_dev + int64_t(kRec) * info->num_tiles;
+  m.part_o = a.part_o;
+  m.part_ml = a.part_ml;
+  m.q_indptr = q_indptr_dev;
+  m.out = a.out;
+  m.o_tok = a.o_tok;
+  m.o_head = a.o_head;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (pool->dtype == KUNSERVE_DTYPE_BF16)
+    return run_prefill<bf16>(a, m, info->num_tiles, info->num_merge,
+                             pages_needed <= kMaxStagedPages, s);
+  return run_prefill<f16>(a, m, info->num_tiles, info->num_merge, pages_needed <= kMaxStagedPages,
+                          s);
 }

@@ -27,7 +27,8 @@ class LlamaOp:
     def __init__(self, max_num_pages: int, layers: int, qo_head: int, kv_head: int,
                  page_size: int, head_size: int, inter_size: int, vocab_size: int,
                  max_batch_size: int, max_batch_tokens: int, max_position_embeddings: int,
-                 tensor_parallel_size: int, device: Optional[torch.device] = None):
+                 tensor_parallel_size: int, device: Optional[torch.device] = None,
+                 dtype: torch.dtype = torch.float16):
         if qo_head % kv_head:
             raise ValueError(f"qo_head {qo_head} is not a multiple of kv_head {kv_head}")
         self.max_num_pages = max_num_pages
@@ -43,7 +44,10 @@ class LlamaOp:
         self.max_position_embeddings = max_position_embeddings
         self.tensor_parallel_size = tensor_parallel_size
         dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
-        self.pool = KVPool.allocate(max_num_pages, layers, kv_head, page_size, head_size, dev)
+        # The model dtype (the reference's --dtype, bf16 by default,
+        # kunserve/kunserve_config.py:61) is the KV pool's dtype.
+        self.pool = KVPool.allocate(max_num_pages, layers, kv_head, page_size, head_size, dev,
+                                    dtype)
 
     # -------------------------------------------------------------- pforward
 

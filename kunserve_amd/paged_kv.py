@@ -40,30 +40,42 @@ def _i32(x) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
 
 
+_DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
+
+
 class KVPool:
     """Separate K and V pools of shape [num_pages, num_layers, num_kv_heads,
-    page_size, head_dim] (any strides with head_dim contiguous)."""
+    page_size, head_dim] (any strides with head_dim contiguous), float16 or
+    bfloat16 (the reference's --dtype, kunserve/kunserve_config.py:61); q,
+    outputs and new K/V passed with a pool must have its dtype."""
 
     def __init__(self, k: torch.Tensor, v: torch.Tensor):
         if k.shape != v.shape or k.stride() != v.stride() or k.dim() != 5:
             raise ValueError("K and V pools must be 5-D with identical shape and strides")
-        if k.dtype != FP16 or v.dtype != FP16:
-            raise ValueError("KV pools must be float16")
+        if k.dtype != v.dtype or k.dtype not in _DTYPES:
+            raise ValueError("KV pools must both be float16 or both bfloat16")
         if k.stride(-1) != 1:
             raise ValueError("head_dim must be contiguous")
         self.k, self.v = k, v
+        self.dtype = k.dtype
         self.num_pages, self.num_layers, self.num_kv_heads, self.page_size, self.head_dim = k.shape
         self._desc = _lib.KVPool(
             k.data_ptr(), v.data_ptr(), self.num_pages, k.stride(0), k.stride(1), k.stride(2),
             k.stride(3), self.num_layers, self.num_kv_heads, self.page_size, self.head_dim,
+            _DTYPES[k.dtype],
         )
 
     @classmethod
     def allocate(cls, num_pages: int, num_layers: int, num_kv_heads: int, page_size: int,
-                 head_dim: int, device="cuda") -> "KVPool":
+                 head_dim: int, device="cuda", dtype: torch.dtype = FP16) -> "KVPool":
         shape = (num_pages, num_layers, num_kv_heads, page_size, head_dim)
-        return cls(torch.empty(shape, dtype=FP16, device=device),
-                   torch.empty(shape, dtype=FP16, device=device))
+        return cls(torch.empty(shape, dtype=dtype, device=device),
+                   torch.empty(shape, dtype=dtype, device=device))
+
+    def check_dtype(self, *tensors: torch.Tensor) -> None:
+        for t in tensors:
+            if t is not None and t.dtype != self.dtype:
+                raise ValueError(f"tensor dtype {t.dtype} does not match the pool's {self.dtype}")
 
     @property
     def device(self) -> torch.device:
@@ -166,8 +178,8 @@ class PageTable:
 def _tensor3(t: torch.Tensor) -> _lib.Tensor3:
     if t.dim() != 3 or t.stride(-1) != 1:
         raise ValueError("expected a [tokens, heads, head_dim] tensor with head_dim contiguous")
-    if t.dtype != FP16:
-        raise ValueError("expected float16")
+    if t.dtype not in _DTYPES:
+        raise ValueError("expected float16 or bfloat16")
     return _lib.Tensor3(t.data_ptr(), t.stride(0), t.stride(1))
 
 
@@ -263,7 +275,7 @@ def kv_pack(pool: KVPool, layer_begin: int, layer_end: int, page_ids,
     n = ids.numel()
     nbytes = int(_lib.lib().kunserve_kv_pack_bytes(pool.desc(), layer_end - layer_begin, n))
     if scratch is None:
-        scratch = torch.empty(max(nbytes // 2, 1), dtype=FP16, device=pool.device)
+        scratch = torch.empty(max(nbytes // 2, 1), dtype=pool.dtype, device=pool.device)
     _lib.call("kunserve_kv_pack", pool.desc(), layer_begin, layer_end, ids.data_ptr(), n,
               scratch.data_ptr(), scratch.numel() * scratch.element_size(),
               _stream_ptr(pool.device))
@@ -317,6 +329,7 @@ def append_kv(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Tensor
         raise ValueError(f"k_new / v_new must be [tokens, {pool.num_kv_heads}, {pool.head_dim}]")
     if q_indptr.numel() != table.num_seqs + 1:
         raise ValueError("q_indptr must have num_seqs + 1 entries")
+    pool.check_dtype(k_new, v_new)
     kd, vd = _tensor3(k_new), _tensor3(v_new)
     _lib.call("kunserve_append_kv", pool.desc(), layer, table.desc(), q_indptr.data_ptr(),
               k_new.shape[0], ctypes.byref(kd), ctypes.byref(vd), _stream_ptr(pool.device))
@@ -348,6 +361,7 @@ def rope_append_kv(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.T
             or inv_freq.device != q.device):
         raise ValueError(f"inv_freq must be {pool.head_dim // 2} float32 values on {q.device}")
     inv_freq = inv_freq.contiguous()
+    pool.check_dtype(q, k_new, v_new)
     qd, kd, vd = _tensor3(q), _tensor3(k_new), _tensor3(v_new)
     _lib.call("kunserve_rope_append_kv", pool.desc(), layer, table.desc(), q_indptr.data_ptr(),
               k_new.shape[0], ctypes.byref(qd), q.shape[1], ctypes.byref(kd), ctypes.byref(vd),
@@ -365,6 +379,7 @@ def paged_decode(pool: KVPool, layer: int, table: PageTable, q: torch.Tensor, pl
                          f"head_dim {pool.head_dim}")
     if out is None:
         out = torch.empty_like(q)
+    pool.check_dtype(q, out)
     scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(pool.head_dim)
     need = plan.workspace_bytes(pool.head_dim)
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
@@ -385,6 +400,7 @@ def paged_prefill(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Te
     """Causal chunked-prefill attention of ragged q [num_tokens, Hq, D]."""
     if out is None:
         out = torch.empty_like(q)
+    pool.check_dtype(q, out)
     scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(pool.head_dim)
     need = plan.workspace_bytes()
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):

@@ -7,25 +7,36 @@ import torch
 from kunserve_amd import KVPool, PageTable
 
 ATOL = 2e-3   # max-abs tolerance for fp16 attention outputs, fp32 accumulation
+# bf16 keeps 8 significant bits to fp16's 11: the same bound scaled by 2^3,
+# rounded up (output rounding alone is up to 2^-9 |o|, and P enters the
+# P.V product as bf16).
+ATOL_BF16 = 2e-2
 
 
 def random_pool(num_pages, num_layers, num_kv_heads, page_size, head_dim, device, seed,
-                scale=1.0) -> KVPool:
+                scale=1.0, dtype=torch.float16) -> KVPool:
     g = torch.Generator(device=device)
     g.manual_seed(seed)
-    pool = KVPool.allocate(num_pages, num_layers, num_kv_heads, page_size, head_dim, device)
+    pool = KVPool.allocate(num_pages, num_layers, num_kv_heads, page_size, head_dim, device,
+                           dtype)
     for t in (pool.k, pool.v):
         # fill layer by layer to bound the temporary fp32 buffer
         for layer in range(num_layers):
             t[:, layer].copy_((torch.randn(t[:, layer].shape, generator=g, device=device,
-                                           dtype=torch.float32) * scale).to(torch.float16))
+                                           dtype=torch.float32) * scale).to(dtype))
     return pool
 
 
-def random_tensor(shape, device, seed, scale=1.0) -> torch.Tensor:
+def random_tensor(shape, device, seed, scale=1.0, dtype=torch.float16) -> torch.Tensor:
     g = torch.Generator(device=device)
     g.manual_seed(seed)
-    return (torch.randn(shape, generator=g, device=device) * scale).to(torch.float16)
+    return (torch.randn(shape, generator=g, device=device) * scale).to(dtype)
+
+
+def to_numpy(t: torch.Tensor) -> np.ndarray:
+    """Host copy; bf16 (which numpy lacks) becomes float32, exactly."""
+    t = t.cpu()
+    return t.float().numpy() if t.dtype == torch.bfloat16 else t.numpy()
 
 
 def compact_for_oracle(pool: KVPool, layer: int, indptr: np.ndarray, indices: np.ndarray,
@@ -38,8 +49,8 @@ def compact_for_oracle(pool: KVPool, layer: int, indptr: np.ndarray, indices: np
     used = np.concatenate(pages) if pages else np.zeros(0, np.int64)
     uniq, inv = np.unique(used, return_inverse=True)
     sel = torch.from_numpy(uniq.astype(np.int64)).to(pool.device)
-    k = pool.k[:, layer].index_select(0, sel)[:, None].cpu().numpy()
-    v = pool.v[:, layer].index_select(0, sel)[:, None].cpu().numpy()
+    k = to_numpy(pool.k[:, layer].index_select(0, sel)[:, None])
+    v = to_numpy(pool.v[:, layer].index_select(0, sel)[:, None])
     new_indptr = np.zeros(len(rows) + 1, dtype=np.int64)
     np.cumsum([len(p) for p in pages], out=new_indptr[1:])
     return k, v, new_indptr, inv.astype(np.int64)
