@@ -467,12 +467,14 @@ __global__ __launch_bounds__(256) void append_kv_kernel(AppendArgs a) {
 
 // Fused prologue of a step: rotary position embedding of q (in place) and
 // of the new k, and the append of the rotated k and of v into the pages.
-// One thread per (token, head slot, 16 dims): head slots [0, Hq) are q
-// heads, [Hq, Hq + Hkv) are KV heads (k rotated and written, v copied).
-// Rotation pairs are (j, j + D/2) with the thread's dims 8c..8c+7 and
-// D/2 + 8c..+7, or (2j, 2j + 1) with dims 16c..16c+15 when interleaved.
-// Angles are the fp32 product position * inv_freq[j]; the rotation runs in
-// fp32 and rounds once.
+// One workgroup per token: its D/2 rotation angles are evaluated once
+// (fp32 product position * inv_freq[j], accurate sincosf) into LDS, then
+// the workgroup streams the token's heads in units of 16 dims: units of
+// head slots [0, Hq) are q heads (rotated in place), of [Hq, Hq + Hkv) KV
+// heads (k rotated and written, the same dims of v copied). Rotation pairs
+// are (j, j + D/2) with a unit's dims 8c..8c+7 and D/2 + 8c..+7, or
+// (2j, 2j + 1) with dims 16c..16c+15 when interleaved. fp32 rotation, one
+// rounding.
 struct RopeArgs {
   f16* q;
   int64_t q_tok, q_head;
@@ -490,7 +492,6 @@ struct RopeArgs {
   const int32_t* q_indptr;
   const float* inv_freq;   // [D / 2]
   int32_t num_seqs;
-  int32_t num_tokens;
   int32_t num_qo_heads;
   int32_t num_kv_heads;
   int32_t head_dim;
@@ -503,18 +504,14 @@ __device__ __forceinline__ void rope_pair(float& a, float& b, float c, float s) 
   b = fmaf(y, c, x * s);
 }
 
+constexpr int kRopeThreads = 256;
+
 template <typename T>
-__global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
+__global__ __launch_bounds__(kRopeThreads) void rope_append_kernel(RopeArgs a) {
   typedef typename Vec<T>::v8 V8;
-  const int units = a.head_dim / 16;   // 16-dim units per head
-  const int64_t per_tok = int64_t(a.num_qo_heads + a.num_kv_heads) * units;
-  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (idx >= int64_t(a.num_tokens) * per_tok) return;
-  const int tok = int(idx / per_tok);
-  if (tok >= a.q_indptr[a.num_seqs]) return;   // tokens not owned by any row
-  const int rem = int(idx % per_tok);
-  const int slot = rem / units;
-  const int c = rem % units;
+  __shared__ float s_cos[128], s_sin[128];   // head_dim <= 256
+  const int tok = blockIdx.x;
+  if (tok >= a.q_indptr[a.num_seqs]) return;   // not owned by any row (uniform)
   int lo = 0, hi = a.num_seqs - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -523,63 +520,63 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
   const int b = lo;
   const int q_len = a.q_indptr[b + 1] - a.q_indptr[b];
   const int pos = a.kv_len[b] - q_len + (tok - a.q_indptr[b]);
-  if (pos < 0 || pos >= a.kv_len[b]) return;
-
-  // The thread's two 8-dim halves and the inv_freq index of each pair.
+  if (pos < 0 || pos >= a.kv_len[b]) return;   // uniform
   const int half = a.head_dim / 2;
-  const int d0 = a.interleave ? 16 * c : 8 * c;
-  const int d1 = a.interleave ? 16 * c + 8 : half + 8 * c;
-  const int f0 = 8 * c;   // first of the thread's 8 pairs
-  float cs[8], sn[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float ang = float(pos) * a.inv_freq[f0 + j];
-    sincosf(ang, &sn[j], &cs[j]);
-  }
-  auto rotate = [&](const V8& x0, const V8& x1, V8& y0, V8& y1) {
-    float u[16];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      u[e] = float(x0[e]);
-      u[8 + e] = float(x1[e]);
-    }
-    if (a.interleave) {
-      // dims 16c + 2j, 16c + 2j + 1 hold pair 8c + j
-#pragma unroll
-      for (int j = 0; j < 8; ++j) rope_pair(u[2 * j], u[2 * j + 1], cs[j], sn[j]);
-    } else {
-      // dims 8c + j and D/2 + 8c + j hold pair 8c + j
-#pragma unroll
-      for (int j = 0; j < 8; ++j) rope_pair(u[j], u[8 + j], cs[j], sn[j]);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      y0[e] = T(u[e]);
-      y1[e] = T(u[8 + e]);
-    }
-  };
+  for (int j = threadIdx.x; j < half; j += kRopeThreads)
+    sincosf(float(pos) * a.inv_freq[j], &s_sin[j], &s_cos[j]);
+  __syncthreads();
 
-  if (slot < a.num_qo_heads) {
-    f16* qp = a.q + int64_t(tok) * a.q_tok + int64_t(slot) * a.q_head;
-    V8 y0, y1;
-    rotate(load_v8<T>(qp + d0), load_v8<T>(qp + d1), y0, y1);
-    *reinterpret_cast<V8*>(qp + d0) = y0;
-    *reinterpret_cast<V8*>(qp + d1) = y1;
-    return;
-  }
-  const int head = slot - a.num_qo_heads;
   const int p = a.indices[a.indptr[b] + (pos >> a.page_shift)];
-  if (p < 0 || p >= a.num_pages) return;
-  const int64_t dst = int64_t(p) * a.page_stride + int64_t(head) * a.head_stride +
+  const bool page_ok = p >= 0 && p < a.num_pages;
+  const int64_t dst = int64_t(page_ok ? p : 0) * a.page_stride +
                       int64_t(pos & ((1 << a.page_shift) - 1)) * a.token_stride;
-  const f16* kp = a.k_new + int64_t(tok) * a.k_tok + int64_t(head) * a.k_head;
-  const f16* vp = a.v_new + int64_t(tok) * a.v_tok + int64_t(head) * a.v_head;
-  V8 y0, y1;
-  rotate(load_v8<T>(kp + d0), load_v8<T>(kp + d1), y0, y1);
-  *reinterpret_cast<V8*>(a.k + dst + d0) = y0;
-  *reinterpret_cast<V8*>(a.k + dst + d1) = y1;
-  store_f16x8(a.v + dst + d0, load_f16x8(vp + d0));
-  store_f16x8(a.v + dst + d1, load_f16x8(vp + d1));
+  const int units = a.head_dim / 16;
+  const int n_units = (a.num_qo_heads + a.num_kv_heads) * units;
+  for (int u = threadIdx.x; u < n_units; u += kRopeThreads) {
+    const int slot = u / units, c = u % units;
+    const int d0 = a.interleave ? 16 * c : 8 * c;
+    const int d1 = a.interleave ? 16 * c + 8 : half + 8 * c;
+    auto rotate = [&](const V8& x0, const V8& x1, V8& y0, V8& y1) {
+      float w[16];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        w[e] = float(x0[e]);
+        w[8 + e] = float(x1[e]);
+      }
+      if (a.interleave) {
+        // dims 16c + 2j, 16c + 2j + 1 hold pair 8c + j
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rope_pair(w[2 * j], w[2 * j + 1], s_cos[8 * c + j], s_sin[8 * c + j]);
+      } else {
+        // dims 8c + j and D/2 + 8c + j hold pair 8c + j
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rope_pair(w[j], w[8 + j], s_cos[8 * c + j], s_sin[8 * c + j]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y0[e] = T(w[e]);
+        y1[e] = T(w[8 + e]);
+      }
+    };
+    V8 y0, y1;
+    if (slot < a.num_qo_heads) {
+      f16* qp = a.q + int64_t(tok) * a.q_tok + int64_t(slot) * a.q_head;
+      rotate(load_v8<T>(qp + d0), load_v8<T>(qp + d1), y0, y1);
+      *reinterpret_cast<V8*>(qp + d0) = y0;
+      *reinterpret_cast<V8*>(qp + d1) = y1;
+      continue;
+    }
+    if (!page_ok) continue;
+    const int head = slot - a.num_qo_heads;
+    const int64_t hd = dst + int64_t(head) * a.head_stride;
+    const f16* kp = a.k_new + int64_t(tok) * a.k_tok + int64_t(head) * a.k_head;
+    const f16* vp = a.v_new + int64_t(tok) * a.v_tok + int64_t(head) * a.v_head;
+    rotate(load_v8<T>(kp + d0), load_v8<T>(kp + d1), y0, y1);
+    *reinterpret_cast<V8*>(a.k + hd + d0) = y0;
+    *reinterpret_cast<V8*>(a.k + hd + d1) = y1;
+    store_f16x8(a.v + hd + d0, load_f16x8(vp + d0));
+    store_f16x8(a.v + hd + d1, load_f16x8(vp + d1));
+  }
 }
 
 // Attention (page ids staged in LDS when they fit), then the split merge.
@@ -652,21 +649,17 @@ extern "C" int kunserve_rope_append_kv(const kunserve_kv_pool* pool, int32_t lay
   a.q_indptr = q_indptr_dev;
   a.inv_freq = inv_freq_dev;
   a.num_seqs = table->num_seqs;
-  a.num_tokens = num_tokens;
   a.num_qo_heads = num_qo_heads;
   a.num_kv_heads = pool->num_kv_heads;
   a.head_dim = pool->head_dim;
   a.interleave = interleave != 0;
-  const int64_t threads =
-      int64_t(num_tokens) * (num_qo_heads + pool->num_kv_heads) * (pool->head_dim / 16);
-  const int64_t blocks = (threads + 255) / 256;
-  KSV_CHECK_ARG(blocks < (int64_t(1) << 31), "rope append too large for one launch");
+  // One workgroup per token.
   if (pool->dtype == KUNSERVE_DTYPE_BF16)
-    rope_append_kernel<bf16>
-        <<<dim3(unsigned(blocks)), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
+    rope_append_kernel<bf16><<<dim3(unsigned(num_tokens)), kRopeThreads, 0,
+                               reinterpret_cast<hipStream_t>(stream)>>>(a);
   else
-    rope_append_kernel<f16>
-        <<<dim3(unsigned(blocks)), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
+    rope_append_kernel<f16><<<dim3(unsigned(num_tokens)), kRopeThreads, 0,
+                              reinterpret_cast<hipStream_t>(stream)>>>(a);
   KSV_CHECK_LAUNCH();
   return KUNSERVE_OK;
 }
