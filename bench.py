@@ -14,7 +14,9 @@ utilisation of the fp16 dense peak; `gqa_decode` — Llama-3-8B GQA decode
 (32/8 heads, batch 128, contexts U[1024, 8192]) as HBM bandwidth; `remap` —
 the 8192-block remap copy as HBM bandwidth and a Llama-2-70B layer decode
 (64/8 heads, batch 256) on the remapped tables, bit-exact against the
-original tables.
+original tables; `pmm` — the Llama-2-7B decode on a pool whose last 784
+pages are 16 dropped Llama-2-7B weight layers (pmm_drop), with the drop and
+restore time per layer.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
 """
@@ -216,6 +218,67 @@ def bench_remap(args, device):
                        "bit_exact_vs_original_tables": same}}
 
 
+# Llama-2-7B layer weights: q/k/v/o 4 x 4096^2, gate/up/down 3 x 4096 x 11008,
+# two RMSNorm vectors, fp16.
+LLAMA2_7B_LAYER_BYTES = 2 * (4 * 4096 * 4096 + 3 * 4096 * 11008 + 2 * 4096)
+
+
+def bench_pmm(args, device):
+    """The Llama-2-7B decode workload on a pool that pmm_drop grew: the last
+    pages of the 16384-page pool come from 16 dropped Llama-2-7B layers
+    (49 pages each), so tables address base and extend pages alike. Times
+    drop and restore per layer and the decode sweep over the grown pool."""
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+
+    w = workloads.llama2_7b_decode()
+    page_bytes = w.num_layers * w.num_kv_heads * w.page_size * w.head_dim * 2
+    per_layer = -(-LLAMA2_7B_LAYER_BYTES // (2 * page_bytes))
+    dropped_layers = 16
+    extend = per_layer * dropped_layers
+    pm = ks.PmmPool(w.num_pages - extend, w.num_layers, w.num_kv_heads, w.page_size,
+                    w.head_dim, extend, device)
+    try:
+        segs = [pm.add_segment(LLAMA2_7B_LAYER_BYTES) for _ in range(dropped_layers)]
+        drop_ms = []
+        for sid in segs:
+            t0 = time.perf_counter()
+            pm.drop(sid)
+            drop_ms.append((time.perf_counter() - t0) * 1e3)
+        assert pm.num_pages == w.num_pages
+        gen = torch.Generator(device=device)
+        gen.manual_seed(w.seed)
+        fill_random_(pm.pool.k, gen)
+        fill_random_(pm.pool.v, gen)
+        res = measure_decode(w, pm.pool, list(range(w.num_layers)), args, device)
+        err = check_decode_sample(res, device)
+        indptr, indices = w.csr()
+        on_extend = int((indices >= w.num_pages - extend).sum())
+        del res["pool"], res["qs"], res["table"]
+        torch.cuda.synchronize()
+        restore_ms = []
+        for _ in segs:
+            t0 = time.perf_counter()
+            pm.restore()
+            restore_ms.append((time.perf_counter() - t0) * 1e3)
+    finally:
+        pm.close()
+    log(f"pmm: {dropped_layers} Llama-2-7B layers dropped into {extend} extend pages; drop "
+        f"{np.mean(drop_ms):.2f} ms/layer, restore {np.mean(restore_ms):.2f} ms/layer; decode "
+        f"over the grown pool ({on_extend} of {len(indices)} table pages on extend pages): "
+        f"per launch {res['launch_ms'] * 1e3:.1f} us = {res['achieved']:.1f} GB/s "
+        f"({res['achieved'] / HBM_PEAK_GBS * 100:.1f}% of HBM peak), max-abs {err:.1e}")
+    if err > 2e-3:
+        print(f"decode on the grown pool failed its check: max-abs {err}", file=sys.stderr)
+        sys.exit(1)
+    return {"workload": f"{w.name} on a pool grown by {dropped_layers} dropped Llama-2-7B layers",
+            "extend_pages": extend, "table_pages_on_extend": on_extend,
+            "drop_ms_per_layer": float(np.mean(drop_ms)),
+            "restore_ms_per_layer": float(np.mean(restore_ms)),
+            "decode_launch_us": res["launch_ms"] * 1e3, "decode_gbs": res["achieved"],
+            "hbm_frac": res["achieved"] / HBM_PEAK_GBS, "decode_max_abs": err}
+
+
 def check_decode_sample(res, device) -> float:
     """Max-abs error of a few rows of layer 0 against the CPU oracle."""
     from oracle import paged_attention_ref as ref
@@ -374,7 +437,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
-    ap.add_argument("--only", choices=["decode", "prefill", "gqa", "remap"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "gqa", "remap", "pmm"],
+                    default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     args = ap.parse_args()
@@ -402,6 +466,9 @@ def main():
     if args.only == "remap":
         print(json.dumps({"remap": bench_remap(args, device)}))
         return
+    if args.only == "pmm":
+        print(json.dumps({"pmm": bench_pmm(args, device)}))
+        return
 
     dec = bench_decode(args, device)
     err = check_decode_sample(dec, device)
@@ -416,13 +483,15 @@ def main():
     w = dec["workload"]
     del dec["pool"], dec["qs"]
     torch.cuda.empty_cache()
-    prefill = gqa = remap = None
+    prefill = gqa = remap = pmm = None
     if args.only is None:
         prefill = bench_prefill(args, device)
         torch.cuda.empty_cache()
         gqa = bench_gqa(args, device)
         torch.cuda.empty_cache()
         remap = bench_remap(args, device)
+        torch.cuda.empty_cache()
+        pmm = bench_pmm(args, device)
         torch.cuda.empty_cache()
 
     line = {
@@ -461,6 +530,7 @@ def main():
         "prefill": prefill,
         "gqa_decode": gqa,
         "remap": remap,
+        "pmm": pmm,
     }
     print(json.dumps(line))
 

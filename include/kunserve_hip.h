@@ -18,7 +18,9 @@
  *   - Pointers named *_dev are device pointers, *_host are host pointers.
  *   - All device work is enqueued on the given stream; no function
  *     synchronises the device or the stream, and no function allocates
- *     device memory: scratch space is passed in by the caller.
+ *     device memory: scratch space is passed in by the caller. The one
+ *     exception is the kunserve_pmm_* group, whose purpose is to create and
+ *     remap device memory; it runs while the engine is paused.
  *   - KV data is fp16 or bf16 (kunserve_kv_pool.dtype; q, outputs and new
  *     K/V share it). Element (page, layer, kv_head, slot, dim) of the K (or
  *     V) pool lives at
@@ -276,6 +278,54 @@ int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
                            const kunserve_prefill_plan_info* info,
                            void* workspace_dev, int64_t workspace_bytes,
                            kunserve_stream_t stream);
+
+/* ------------------------------------ parameter memory remap (pmm_drop) */
+
+/* KV pools whose tail can be extended by the memory of dropped weight
+ * layers, and given back (LlamaOp.pmm_drop / pmm_restore,
+ * kunserve/worker.py:454-501, kunserve/flash_backend.py:716-725; the remap
+ * is described at kunserve/llm_engine.py:553-558). The K and V pools are
+ * address ranges reserved for base + max_extend pages of page_bytes each,
+ * of which the first num_pages are mapped; a kunserve_kv_pool built on them
+ * must carry that num_pages. These calls are synchronous on the host:
+ * drop and restore wait for all work on the device to finish before they
+ * move memory, and must not run concurrently with each other or with work
+ * submitted from other threads. */
+typedef struct kunserve_pmm kunserve_pmm;
+
+/* Reserves the two ranges on `device` and maps base_pages of fresh device
+ * memory at the start of each. page_bytes must be a multiple of the
+ * device's mapping granularity (4 KiB on MI355X). */
+int kunserve_pmm_create(int32_t device, int64_t page_bytes,
+                        int64_t base_pages, int64_t max_extend_pages,
+                        kunserve_pmm** out);
+
+/* Allocates a weight segment of `bytes` (a multiple of 2 * page_bytes)
+ * and maps it at an address of its own, returned in *address, where the
+ * caller keeps one layer's weights. */
+int kunserve_pmm_add_segment(kunserve_pmm* pmm, int64_t bytes,
+                             int32_t* segment_id, void** address);
+
+/* Drops a weight segment: its first half becomes K pages
+ * [num_pages, num_pages + n) and its second half the V pages of the same
+ * ids, n = bytes / (2 * page_bytes); the new page count is returned. The
+ * segment's address stops being valid; the new pages hold its bytes
+ * unchanged (the extend blocks of kunserve/block_manager.py:262-269). */
+int kunserve_pmm_drop(kunserve_pmm* pmm, int32_t segment_id,
+                      int64_t* num_pages);
+
+/* Undoes the most recent drop: the pool's last n pages become the segment
+ * again, at its original address and holding what those pages held. */
+int kunserve_pmm_restore(kunserve_pmm* pmm, int32_t* segment_id,
+                         int64_t* num_pages);
+
+/* Current K and V pool bases (fixed for the handle's life) and page
+ * count. */
+int kunserve_pmm_pools(const kunserve_pmm* pmm, void** k, void** v,
+                       int64_t* num_pages);
+
+/* Waits for the device, unmaps and frees every pool page and segment. */
+void kunserve_pmm_destroy(kunserve_pmm* pmm);
 
 #ifdef __cplusplus
 }

@@ -10,15 +10,16 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .llama_op import LlamaOp
+from .llama_op import LlamaOp, kept_layers
 from .paged_kv import (AttentionStep, DecodePlan, KVPool, PageTable, PrefillPlan, append_kv,
                        copy_blocks, csr_from_lists, kv_lens_for_step, kv_pack, kv_scatter,
                        paged_decode, paged_prefill, rope_append_kv, rope_inv_freq, swap)
+from .pmm import PmmPool
 
 __all__ = [
-    "AttentionStep", "DecodePlan", "KVPool", "LlamaOp", "PageTable", "PrefillPlan",
+    "AttentionStep", "DecodePlan", "KVPool", "LlamaOp", "PageTable", "PmmPool", "PrefillPlan",
     "append_kv", "copy_blocks", "csr_from_lists", "kv_lens_for_step", "kv_pack",
-    "kv_scatter", "paged_decode", "paged_prefill", "rope_append_kv", "rope_inv_freq", "swap",
+    "kept_layers", "kv_scatter", "paged_decode", "paged_prefill", "rope_append_kv", "rope_inv_freq", "swap",
     "library_path",
 ]
 

@@ -93,6 +93,14 @@ SIGNATURES = {
                                        POINTER(Tensor3), POINTER(Tensor3), c_int32, c_float,
                                        c_void_p, POINTER(PrefillPlanInfo), c_void_p, c_int64,
                                        c_void_p]),
+    "kunserve_pmm_create": (c_int, [c_int32, c_int64, c_int64, c_int64, POINTER(c_void_p)]),
+    "kunserve_pmm_add_segment": (c_int, [c_void_p, c_int64, POINTER(c_int32),
+                                         POINTER(c_void_p)]),
+    "kunserve_pmm_drop": (c_int, [c_void_p, c_int32, POINTER(c_int64)]),
+    "kunserve_pmm_restore": (c_int, [c_void_p, POINTER(c_int32), POINTER(c_int64)]),
+    "kunserve_pmm_pools": (c_int, [c_void_p, POINTER(c_void_p), POINTER(c_void_p),
+                                   POINTER(c_int64)]),
+    "kunserve_pmm_destroy": (None, [c_void_p]),
 }
 
 _lib: ctypes.CDLL | None = None

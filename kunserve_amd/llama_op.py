@@ -15,12 +15,25 @@ run(layer, q, k, v) is the per-layer attention stage.
 """
 from __future__ import annotations
 
-from typing import List, Optional, Sequence
+from typing import Dict, List, Optional, Sequence
 
 import numpy as np
 import torch
 
 from .paged_kv import AttentionStep, KVPool, copy_blocks, kv_pack, kv_scatter
+from .pmm import PmmPool
+
+
+def kept_layers(layers: int, rank_in_group: int, num_group_instances: int) -> range:
+    """Layers instance rank_in_group of a balloon group of num_group_instances
+    keeps: the group splits the model into equal contiguous pipeline stages
+    (kunserve/flash_backend.py:2395,2442-2443)."""
+    if num_group_instances < 1 or not 0 <= rank_in_group < num_group_instances:
+        raise ValueError(f"rank {rank_in_group} outside a group of {num_group_instances}")
+    if layers % num_group_instances:
+        raise ValueError(f"{layers} layers do not split into {num_group_instances} equal stages")
+    per = layers // num_group_instances
+    return range(rank_in_group * per, (rank_in_group + 1) * per)
 
 
 class LlamaOp:
@@ -28,7 +41,7 @@ class LlamaOp:
                  page_size: int, head_size: int, inter_size: int, vocab_size: int,
                  max_batch_size: int, max_batch_tokens: int, max_position_embeddings: int,
                  tensor_parallel_size: int, device: Optional[torch.device] = None,
-                 dtype: torch.dtype = torch.float16):
+                 dtype: torch.dtype = torch.float16, max_extend_pages: int = 0):
         if qo_head % kv_head:
             raise ValueError(f"qo_head {qo_head} is not a multiple of kv_head {kv_head}")
         self.max_num_pages = max_num_pages
@@ -46,8 +59,19 @@ class LlamaOp:
         dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
         # The model dtype (the reference's --dtype, bf16 by default,
         # kunserve/kunserve_config.py:61) is the KV pool's dtype.
-        self.pool = KVPool.allocate(max_num_pages, layers, kv_head, page_size, head_size, dev,
-                                    dtype)
+        # With max_extend_pages > 0 the pool can grow by the memory of
+        # dropped weight layers (pmm_drop); layer_weights() hands out that
+        # memory.
+        self.num_base_pages = max_num_pages
+        self.pmm: Optional[PmmPool] = None
+        self._weight_segments: Dict[int, int] = {}   # layer -> segment id
+        if max_extend_pages > 0:
+            self.pmm = PmmPool(max_num_pages, layers, kv_head, page_size, head_size,
+                               max_extend_pages, dev, dtype)
+            self.pool = self.pmm.pool
+        else:
+            self.pool = KVPool.allocate(max_num_pages, layers, kv_head, page_size, head_size,
+                                        dev, dtype)
 
     # -------------------------------------------------------------- pforward
 
@@ -82,6 +106,67 @@ class LlamaOp:
                              is_prefill_requests, pages_of_reqs)
         step.layer_range = (local_layer_start, local_layer_end)
         return step
+
+    # ------------------------------------------------- parameter memory
+
+    def layer_weights(self, layer: int, nbytes: int) -> torch.Tensor:
+        """Device memory (uint8, at least nbytes, rounded up to whole block
+        pairs) for the weights of one layer, which pmm_drop can turn into KV
+        blocks. Valid while the layer is not dropped."""
+        if self.pmm is None:
+            raise RuntimeError("LlamaOp was built without max_extend_pages")
+        if not 0 <= layer < self.layers:
+            raise ValueError(f"layer {layer} outside the model")
+        if layer not in self._weight_segments:
+            self._weight_segments[layer] = self.pmm.add_segment(nbytes)
+        elif self.pmm.segment_pages(self._weight_segments[layer]) * 2 * self.pmm.page_bytes < nbytes:
+            raise ValueError(f"layer {layer} already holds a smaller weight segment")
+        return self.pmm.segment(self._weight_segments[layer])
+
+    def pmm_drop(self, rank_in_group: int, num_group_instances: int) -> int:
+        """Drops the weights of every layer outside this instance's stage and
+        returns the number of KV blocks they became (kunserve/worker.py:454-458).
+        The new blocks are [num_base, num_base + returned) in order of the
+        dropped layers (kunserve/block_manager.py:262-269); K blocks take the
+        first half of each layer's memory and V blocks the second. Waits for
+        the device. Views of the dropped weights must not be used afterwards."""
+        if self.pmm is None:
+            raise RuntimeError("LlamaOp was built without max_extend_pages")
+        keep = kept_layers(self.layers, rank_in_group, num_group_instances)
+        dropped = set(self.dropped_layers())
+        added = 0
+        for layer in sorted(self._weight_segments):
+            if layer in keep or layer in dropped:
+                continue
+            added += len(self.pmm.drop(self._weight_segments[layer]))
+        self._sync_pool()
+        return added
+
+    def pmm_restore(self) -> List[int]:
+        """Maps every dropped layer's memory back to its weights and returns
+        those layers (kunserve/worker.py:484-487); their blocks leave the
+        pool, so no request may hold them. The memory comes back holding KV
+        data: the weights themselves are reloaded by the caller (the
+        reference pulls them from a peer instance over NCCL,
+        kunserve/llm_engine.py:553-558)."""
+        if self.pmm is None:
+            raise RuntimeError("LlamaOp was built without max_extend_pages")
+        by_segment = {sid: layer for layer, sid in self._weight_segments.items()}
+        restored = []
+        while self.pmm.dropped:
+            restored.append(by_segment[self.pmm.restore()])
+        self._sync_pool()
+        return sorted(restored)
+
+    def dropped_layers(self) -> List[int]:
+        if self.pmm is None:
+            return []
+        by_segment = {sid: layer for layer, sid in self._weight_segments.items()}
+        return sorted(by_segment[s] for s in self.pmm.dropped)
+
+    def _sync_pool(self) -> None:
+        self.pool = self.pmm.pool
+        self.max_num_pages = self.pmm.num_pages
 
     # ------------------------------------------------------ block movement
 

@@ -49,7 +49,9 @@ class KVPool:
     bfloat16 (the reference's --dtype, kunserve/kunserve_config.py:61); q,
     outputs and new K/V passed with a pool must have its dtype."""
 
-    def __init__(self, k: torch.Tensor, v: torch.Tensor):
+    def __init__(self, k: torch.Tensor, v: torch.Tensor, owner=None):
+        """owner: the PmmPool whose memory k and v view, if any; the view
+        stops being usable once that pool's pages are remapped."""
         if k.shape != v.shape or k.stride() != v.stride() or k.dim() != 5:
             raise ValueError("K and V pools must be 5-D with identical shape and strides")
         if k.dtype != v.dtype or k.dtype not in _DTYPES:
@@ -64,6 +66,8 @@ class KVPool:
             k.stride(3), self.num_layers, self.num_kv_heads, self.page_size, self.head_dim,
             _DTYPES[k.dtype],
         )
+        self._owner = owner
+        self._generation = owner.generation if owner is not None else 0
 
     @classmethod
     def allocate(cls, num_pages: int, num_layers: int, num_kv_heads: int, page_size: int,
@@ -87,6 +91,9 @@ class KVPool:
         return 2 * self.num_layers * self.num_kv_heads * self.page_size * self.head_dim * 2
 
     def desc(self) -> ctypes.pointer:
+        if self._owner is not None and self._owner.generation != self._generation:
+            raise RuntimeError("this KVPool predates a pmm drop or restore of its pages; "
+                               "use the owner's current pool")
         return ctypes.byref(self._desc)
 
 

@@ -74,3 +74,31 @@ def test_remap_tables_point_at_copies():
     allp = np.concatenate(r.decode.pages)
     assert not np.any((allp >= 8192) & (allp < 16384))
     assert any(int(x) in src_set for x in allp)
+
+
+def test_kept_layers_follow_the_stage_split():
+    """kunserve/flash_backend.py:2395,2442-2443: instance r of g runs layers
+    [r * L // g, (r + 1) * L // g); pmm_drop drops the others."""
+    from kunserve_amd import kept_layers
+
+    assert kept_layers(32, 0, 1) == range(0, 32)
+    assert kept_layers(32, 0, 2) == range(0, 16)
+    assert kept_layers(32, 1, 2) == range(16, 32)
+    assert kept_layers(80, 3, 4) == range(60, 80)
+    # every layer is kept by exactly one instance of the group
+    for g in (1, 2, 4, 8):
+        owners = sorted(l for r in range(g) for l in kept_layers(32, r, g))
+        assert owners == list(range(32))
+    with pytest.raises(ValueError):
+        kept_layers(30, 0, 4)
+    with pytest.raises(ValueError):
+        kept_layers(32, 2, 2)
+
+
+def test_pmm_pool_needs_a_gpu_device():
+    import torch
+
+    from kunserve_amd import PmmPool
+
+    with pytest.raises(ValueError, match="GPU device"):
+        PmmPool(8, 2, 2, 16, 128, 8, device=torch.device("cpu"))
