@@ -16,7 +16,8 @@ the 8192-block remap copy as HBM bandwidth and a Llama-2-70B layer decode
 (64/8 heads, batch 256) on the remapped tables, bit-exact against the
 original tables; `pmm` — the Llama-2-7B decode on a pool whose last 784
 pages are 16 dropped Llama-2-7B weight layers (pmm_drop), with the drop and
-restore time per layer.
+restore time per layer; `swap` — 512 random blocks swapped out to pinned
+host memory and back, against a contiguous copy over the same link.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
 """
@@ -418,6 +419,69 @@ def bench_prefill(args, device):
                             "gbs": rope_bytes / (rope_ms * 1e-3) / 1e9}}
 
 
+# -------------------------------------------------------------------- swap
+
+
+def bench_swap(args, device):
+    """Block swap (torch.ops.swapping_ops.swap) between the GPU pool and a
+    pinned host pool, both directions, on blocks of the remap workload's
+    shape ([32 layers, 8 KV heads, 16, 128] fp16 = 1 MiB per K or V block).
+    The copies run on the DMA engines over the host link, so the roofline is
+    the link: one contiguous pinned copy of the same byte count, timed the
+    same way, is the reference rate."""
+    import kunserve_amd as ks
+
+    shape = (32, 8, 16, 128)
+    n_gpu, n_cpu, n = 2048, 1024, 512
+    rng = np.random.default_rng(1007)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(1007)
+    kc = torch.empty((n_gpu, *shape), dtype=torch.float16, device=device)
+    vc = torch.empty_like(kc)
+    fill_random_(kc, gen, 0)
+    fill_random_(vc, gen, 0)
+    ksw = torch.empty((n_cpu, *shape), dtype=torch.float16, pin_memory=True)
+    vsw = torch.empty_like(ksw, pin_memory=True)
+    gpu_src = rng.permutation(n_gpu // 2)[:n].tolist()               # from the first half
+    cpu_slot = rng.permutation(n_cpu)[:n].tolist()
+    gpu_dst = (n_gpu // 2 + rng.permutation(n_gpu // 2)[:n]).tolist()  # into the second half
+    nbytes = 2 * n * kc[0].numel() * 2
+
+    def timed(fn, reps=3):
+        best = None
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            t = a.elapsed_time(b)
+            best = t if best is None else min(best, t)
+        return best
+
+    out_ms = timed(lambda: ks.swap(gpu_src, cpu_slot, False, kc, vc, ksw, vsw))
+    in_ms = timed(lambda: ks.swap(cpu_slot, gpu_dst, True, kc, vc, ksw, vsw))
+    ok = bool(torch.equal(kc[gpu_dst].view(torch.int16), kc[gpu_src].view(torch.int16)) and
+              torch.equal(vc[gpu_dst].view(torch.int16), vc[gpu_src].view(torch.int16)))
+    # Link reference: one contiguous pinned copy of the same byte count.
+    dev_buf = kc[:2 * n].reshape(-1)
+    host_buf = torch.empty(dev_buf.numel(), dtype=torch.float16, pin_memory=True)
+    d2h_ms = timed(lambda: host_buf.copy_(dev_buf, non_blocking=True))
+    h2d_ms = timed(lambda: dev_buf.copy_(host_buf, non_blocking=True))
+    gbs = lambda ms: nbytes / (ms * 1e-3) / 1e9
+    res = {"workload": f"swap {n} blocks of 2 x 1 MiB (K and V) GPU<->pinned host",
+           "out_gbs": gbs(out_ms), "in_gbs": gbs(in_ms),
+           "link_d2h_gbs": gbs(d2h_ms), "link_h2d_gbs": gbs(h2d_ms),
+           "out_frac_of_link": d2h_ms / out_ms, "in_frac_of_link": h2d_ms / in_ms,
+           "bit_exact_round_trip": ok}
+    log(f"swap: out {res['out_gbs']:.1f} GB/s ({res['out_frac_of_link'] * 100:.0f}% of a "
+        f"contiguous D2H copy, {res['link_d2h_gbs']:.1f} GB/s); in {res['in_gbs']:.1f} GB/s "
+        f"({res['in_frac_of_link'] * 100:.0f}% of H2D, {res['link_h2d_gbs']:.1f} GB/s); "
+        f"round trip bit-exact: {ok}")
+    del kc, vc, ksw, vsw, host_buf
+    return res
+
+
 def load_traffic():
     """HBM bytes per decode launch measured by rocprofv3 (FETCH_SIZE and
     WRITE_SIZE passes, scaled by a known-size copy); None if not recorded."""
@@ -437,7 +501,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
-    ap.add_argument("--only", choices=["decode", "prefill", "gqa", "remap", "pmm"],
+    ap.add_argument("--only", choices=["decode", "prefill", "gqa", "remap", "pmm", "swap"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
@@ -469,6 +533,9 @@ def main():
     if args.only == "pmm":
         print(json.dumps({"pmm": bench_pmm(args, device)}))
         return
+    if args.only == "swap":
+        print(json.dumps({"swap": bench_swap(args, device)}))
+        return
 
     dec = bench_decode(args, device)
     err = check_decode_sample(dec, device)
@@ -483,7 +550,7 @@ def main():
     w = dec["workload"]
     del dec["pool"], dec["qs"]
     torch.cuda.empty_cache()
-    prefill = gqa = remap = pmm = None
+    prefill = gqa = remap = pmm = swp = None
     if args.only is None:
         prefill = bench_prefill(args, device)
         torch.cuda.empty_cache()
@@ -492,6 +559,8 @@ def main():
         remap = bench_remap(args, device)
         torch.cuda.empty_cache()
         pmm = bench_pmm(args, device)
+        torch.cuda.empty_cache()
+        swp = bench_swap(args, device)
         torch.cuda.empty_cache()
 
     line = {
@@ -531,6 +600,7 @@ def main():
         "gqa_decode": gqa,
         "remap": remap,
         "pmm": pmm,
+        "swap": swp,
     }
     print(json.dumps(line))
 

@@ -8,6 +8,10 @@
 // ranges) addressed through an optional id list on each side, and each
 // workgroup streams a chunk of one span with 16-byte vector loads, eight
 // loads in flight per lane before the first store.
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
 #include "common.hpp"
 
 namespace kunserve {
@@ -240,6 +244,86 @@ extern "C" int kunserve_kv_scatter(const kunserve_kv_pool* pool, int32_t layer_b
                          scratch_bytes, false, reinterpret_cast<hipStream_t>(stream));
 }
 
+namespace {
+// Pinned host slots that hold a swap's (src, dst) id lists while its copy
+// kernels read them. A slot is reused once the event recorded after its
+// kernels has completed (hipEventQuery: no host wait); when every slot is
+// still in flight a new one is allocated, up to kMaxSwapSlots, after which
+// the oldest is waited for. Slots are per device and live until the
+// process ends.
+struct SwapIdSlot {
+  int32_t* ids = nullptr;
+  int64_t cap = 0;
+  hipEvent_t done = nullptr;
+  int device = -1;
+  uint64_t used = 0;   // order of last use
+  bool busy = false;   // handed out, event not yet recorded
+};
+constexpr size_t kMaxSwapSlots = 64;
+std::mutex g_swap_mu;
+std::vector<SwapIdSlot> g_swap_slots;
+uint64_t g_swap_clock = 0;
+
+int acquire_swap_ids(int64_t count, hipStream_t s, int32_t** out) {
+  int dev = 0;
+  KSV_CHECK_HIP(hipStreamGetDevice(s, &dev));
+  std::lock_guard<std::mutex> lock(g_swap_mu);
+  SwapIdSlot* pick = nullptr;
+  SwapIdSlot* oldest = nullptr;
+  size_t on_dev = 0;
+  for (SwapIdSlot& sl : g_swap_slots) {
+    if (sl.device != dev || sl.busy) continue;
+    ++on_dev;
+    if (!oldest || sl.used < oldest->used) oldest = &sl;
+    if (!pick && hipEventQuery(sl.done) == hipSuccess) pick = &sl;
+  }
+  (void)hipGetLastError();   // hipEventQuery reports hipErrorNotReady as an error
+  if (!pick && on_dev >= kMaxSwapSlots && oldest) {
+    KSV_CHECK_HIP(hipEventSynchronize(oldest->done));
+    pick = oldest;
+  }
+  if (!pick) {
+    int cur = 0;
+    KSV_CHECK_HIP(hipGetDevice(&cur));
+    if (cur != dev) KSV_CHECK_HIP(hipSetDevice(dev));
+    SwapIdSlot sl;
+    sl.device = dev;
+    const hipError_t e = hipEventCreateWithFlags(&sl.done, hipEventDisableTiming);
+    if (cur != dev) (void)hipSetDevice(cur);
+    KSV_CHECK_HIP(e);
+    g_swap_slots.push_back(sl);
+    pick = &g_swap_slots.back();
+  }
+  if (pick->cap < count) {
+    if (pick->ids) KSV_CHECK_HIP(hipHostFree(pick->ids));
+    pick->ids = nullptr;
+    pick->cap = 0;
+    const int64_t cap = std::max<int64_t>(count, 4096);
+    KSV_CHECK_HIP(hipHostMalloc(reinterpret_cast<void**>(&pick->ids), cap * sizeof(int32_t),
+                                hipHostMallocDefault));
+    pick->cap = cap;
+  }
+  pick->busy = true;
+  pick->used = ++g_swap_clock;
+  *out = pick->ids;
+  return KUNSERVE_OK;
+}
+
+// Hands the slot holding `ids` back; when `launched`, it stays in use until
+// the work now on stream s completes.
+int release_swap_ids(int32_t* ids, hipStream_t s, bool launched) {
+  std::lock_guard<std::mutex> lock(g_swap_mu);
+  for (SwapIdSlot& sl : g_swap_slots) {
+    if (sl.ids != ids) continue;
+    sl.busy = false;
+    if (launched) KSV_CHECK_HIP(hipEventRecord(sl.done, s));
+    return KUNSERVE_OK;
+  }
+  set_error("swap id slot not found");
+  return KUNSERVE_EINVAL;
+}
+}  // namespace
+
 extern "C" int kunserve_swap_blocks(const int64_t* src_ids_host, const int64_t* dst_ids_host,
                                     int64_t n, int32_t is_swap_in, void* k_cache_dev,
                                     void* v_cache_dev, int64_t num_gpu_blocks,
@@ -262,13 +346,51 @@ extern "C" int kunserve_swap_blocks(const int64_t* src_ids_host, const int64_t* 
       return KUNSERVE_ERANGE;
     }
   }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // The host pools are pinned: the copy kernel addresses them directly
+  // (PCIe reads or writes from the CUs), one launch per pool for every
+  // block, which keeps the host link busy; a copy call per block leaves it
+  // idle between calls.
+  void* k_host_dev = nullptr;
+  void* v_host_dev = nullptr;
+  const bool mapped = hipHostGetDevicePointer(&k_host_dev, k_swap_host, 0) == hipSuccess &&
+                      hipHostGetDevicePointer(&v_host_dev, v_swap_host, 0) == hipSuccess &&
+                      k_host_dev && v_host_dev;
+  if (mapped) {
+    (void)hipGetLastError();
+    int32_t* ids = nullptr;
+    int rc = acquire_swap_ids(2 * n, s, &ids);
+    if (rc) return rc;
+    for (int64_t t = 0; t < n; ++t) {
+      ids[t] = int32_t(src_ids_host[t]);
+      ids[n + t] = int32_t(dst_ids_host[t]);
+    }
+    char* srcs[2] = {static_cast<char*>(is_swap_in ? k_host_dev : k_cache_dev),
+                     static_cast<char*>(is_swap_in ? v_host_dev : v_cache_dev)};
+    char* dsts[2] = {static_cast<char*>(is_swap_in ? k_cache_dev : k_host_dev),
+                     static_cast<char*>(is_swap_in ? v_cache_dev : v_host_dev)};
+    CopyJob jobs[2];
+    for (int kv = 0; kv < 2; ++kv) {
+      CopyJob& job = jobs[kv];
+      job = CopyJob{};
+      job.src = {srcs[kv], ids, block_bytes, 0, src_limit};
+      job.dst = {dsts[kv], ids + n, block_bytes, 0, dst_limit};
+      job.n = n;
+      job.spans = 1;
+      job.span_bytes = block_bytes;
+    }
+    rc = launch_jobs(jobs[0], &jobs[1], s);
+    const int rr = release_swap_ids(ids, s, rc == KUNSERVE_OK);
+    return rc ? rc : rr;
+  }
+  (void)hipGetLastError();
+  // Host memory the device cannot address: one DMA copy per run of
+  // consecutive ids.
   char* srcs[2] = {static_cast<char*>(is_swap_in ? k_swap_host : k_cache_dev),
                    static_cast<char*>(is_swap_in ? v_swap_host : v_cache_dev)};
   char* dsts[2] = {static_cast<char*>(is_swap_in ? k_cache_dev : k_swap_host),
                    static_cast<char*>(is_swap_in ? v_cache_dev : v_swap_host)};
   const hipMemcpyKind kind = is_swap_in ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // Merge runs where both source and destination ids are consecutive.
   int64_t i = 0;
   while (i < n) {
     int64_t j = i + 1;

@@ -5,8 +5,9 @@
 // HBM-bound: every K/V byte of a sequence is read exactly once per layer.
 // Design for gfx950 (wave64, 256 CUs):
 //  * The host plan cuts every sequence into partitions of part_tokens and
-//    orders them longest first; the grid is (work items, head groups), so
-//    mixed context lengths still give an even, device-filling grid.
+//    orders them longest first; the grid is work items x head groups, head
+//    groups fastest, so mixed context lengths still give an even,
+//    device-filling grid that is dispatched longest item first.
 //  * A workgroup (4 waves) owns one partition of one KV head and all
 //    `G` query heads that share it (GQA: one KV read serves G heads).
 //  * The partition's slice of the page table is staged in LDS once; after
@@ -57,6 +58,8 @@ struct DecodeArgs {
   float* part_o;            // [slots][num_qo_heads][D]
   float* part_lse;          // [slots][num_qo_heads]
   int32_t num_qo_heads;
+  int32_t head_groups;      // num_qo_heads / G: workgroup b runs head group b % head_groups
+                            // of work item b / head_groups
   int32_t ratio;            // num_qo_heads / num_kv_heads
   float scale_log2;         // sm_scale * log2(e)
 };
@@ -79,9 +82,10 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
   const int row = lane / LPT;
   const int col = lane % LPT;
 
-  const int32_t* w = a.work + 4 * blockIdx.x;
+  const int item = int(blockIdx.x) / a.head_groups;
+  const int32_t* w = a.work + 4 * item;
   const int seq = w[0], tb = w[1], te = w[2], slot = w[3];
-  const int hq0 = blockIdx.y * G;
+  const int hq0 = (int(blockIdx.x) - item * a.head_groups) * G;
   const int hkv = hq0 / a.ratio;
   const int page_mask = (1 << a.page_shift) - 1;
 
@@ -290,9 +294,10 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   const int lrow = lane >> 4;  // load layout: token row within a 4-row load
   const int lcol = lane & 15;  // load layout: 16-byte chunk of the row
 
-  const int32_t* w = a.work + 4 * blockIdx.x;
+  const int item = int(blockIdx.x) / a.head_groups;
+  const int32_t* w = a.work + 4 * item;
   const int seq = w[0], tb = w[1], te = w[2], slot = w[3];
-  const int hq0 = blockIdx.y * G;
+  const int hq0 = (int(blockIdx.x) - item * a.head_groups) * G;
   const int hkv = hq0 / a.ratio;
   const int page_mask = (1 << a.page_shift) - 1;
 
@@ -734,7 +739,15 @@ extern "C" int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer
   a.scale_log2 = sm_scale * 1.4426950408889634f;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  dim3 grid(info->num_work, num_qo_heads / info->group_size);
+  // One dimension, head groups fastest: the dispatch order is then the
+  // plan's longest-first item order for every head at once (a launch ends on
+  // its shortest items), and neighbouring workgroups read neighbouring head
+  // slabs of the same pages.
+  a.head_groups = num_qo_heads / info->group_size;
+  const int64_t nblocks = int64_t(info->num_work) * a.head_groups;
+  KSV_CHECK_ARG(nblocks < (int64_t(1) << 31), "decode grid of %lld workgroups is too large",
+                (long long)nblocks);
+  const dim3 grid(static_cast<unsigned>(nblocks));
   if (pool->dtype == KUNSERVE_DTYPE_BF16)
     return run_decode<bf16>(a, *info, plan_dev, pool->head_dim, num_qo_heads, grid, s);
   return run_decode<f16>(a, *info, plan_dev, pool->head_dim, num_qo_heads, grid, s);

@@ -122,6 +122,47 @@ def test_swap_on_side_stream_is_ordered(device):
     assert torch.equal(ks[2].view(torch.int16), k[1].view(torch.int16).cpu())
 
 
+def test_swap_views_into_larger_pinned_tensors(device):
+    """Host pools that start inside a larger pinned allocation (the caching
+    host allocator hands out such views)."""
+    shape = (6, 2, 2, 16, 128)
+    k = unique_pool(shape, device)
+    v = unique_pool(shape, device, 5)
+    big_k = torch.zeros((9,) + shape[1:], dtype=torch.float16, pin_memory=True)
+    big_v = torch.zeros((9,) + shape[1:], dtype=torch.float16, pin_memory=True)
+    ks, vs = big_k[3:8], big_v[2:7]
+    swap([5, 0, 2], [4, 0, 1], False, k, v, ks, vs)
+    torch.cuda.synchronize()
+    for s_, d in zip([5, 0, 2], [4, 0, 1]):
+        assert torch.equal(ks[d].view(torch.int16), k[s_].view(torch.int16).cpu())
+        assert torch.equal(vs[d].view(torch.int16), v[s_].view(torch.int16).cpu())
+    # nothing outside the views was written
+    assert not big_k[:3].view(torch.int16).any() and not big_k[8:].view(torch.int16).any()
+    assert not big_v[:2].view(torch.int16).any() and not big_v[7:].view(torch.int16).any()
+
+
+def test_many_swaps_in_flight_without_sync(device):
+    """Back-to-back swaps on one stream with no host wait between them: each
+    call's id lists must stay intact until its copies ran, and stream order
+    must hold (the same GPU block goes out, is overwritten, goes out again)."""
+    shape = (8, 1, 2, 16, 64)
+    k = unique_pool(shape, device)
+    v = unique_pool(shape, device, 3)
+    n_calls = 150   # more than the id slots kept per device
+    ks = torch.zeros((n_calls,) + shape[1:], dtype=torch.float16, pin_memory=True)
+    vs = torch.zeros((n_calls,) + shape[1:], dtype=torch.float16, pin_memory=True)
+    want_k = []
+    for c in range(n_calls):
+        src = c % shape[0]
+        k.view(torch.int16)[src].add_(1)   # changes the block between swaps, in stream order
+        want_k.append(k[src].clone())
+        swap([src], [c], False, k, v, ks, vs)
+    torch.cuda.synchronize()
+    for c in range(n_calls):
+        assert torch.equal(ks[c].view(torch.int16), want_k[c].view(torch.int16).cpu()), c
+        assert torch.equal(vs[c].view(torch.int16), v[c % shape[0]].view(torch.int16).cpu()), c
+
+
 def test_pack_scatter_round_trip(device):
     shape = (40, 6, 2, 16, 128)
     a = KVPool(unique_pool(shape, device), unique_pool(shape, device, 4))
