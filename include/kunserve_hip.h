@@ -137,8 +137,12 @@ int64_t kunserve_kv_pack_bytes(const kunserve_kv_pool* pool, int32_t num_layers,
  * for each i, copy whole block src_ids[i] -> dst_ids[i] for K and V.
  * is_swap_in != 0: host (pinned) pool -> device pool; else device -> host.
  * Ids are host arrays. Block b of a pool is the contiguous byte range
- * [b*block_bytes, (b+1)*block_bytes). Consecutive runs of ids are merged
- * into one DMA copy. Enqueued on `stream`; does not synchronise. */
+ * [b*block_bytes, (b+1)*block_bytes). Pinned host pools (hipHostMalloc)
+ * are read or written in place by one copy kernel per pool; the ids are
+ * staged in a pinned slot the library keeps per device (reused once the
+ * copies that read it have completed, a host wait only when 64 swaps are in
+ * flight). Host memory the device cannot map falls back to one DMA copy per
+ * run of consecutive ids. Enqueued on `stream`; does not synchronise. */
 int kunserve_swap_blocks(const int64_t* src_ids_host,
                          const int64_t* dst_ids_host, int64_t n,
                          int32_t is_swap_in, void* k_cache_dev,
