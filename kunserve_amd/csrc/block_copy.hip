@@ -266,7 +266,10 @@ uint64_t g_swap_clock = 0;
 
 int acquire_swap_ids(int64_t count, hipStream_t s, int32_t** out) {
   int dev = 0;
-  KSV_CHECK_HIP(hipStreamGetDevice(s, &dev));
+  if (s)
+    KSV_CHECK_HIP(hipStreamGetDevice(s, &dev));
+  else
+    KSV_CHECK_HIP(hipGetDevice(&dev));   // the null stream of the current device
   std::lock_guard<std::mutex> lock(g_swap_mu);
   SwapIdSlot* pick = nullptr;
   SwapIdSlot* oldest = nullptr;

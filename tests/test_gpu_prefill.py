@@ -97,6 +97,24 @@ def test_prefill_split_kv_matches_oracle(device, ps):
     assert max_abs(out_s, want) <= ATOL
 
 
+@pytest.mark.parametrize("ps", [4, 256])
+def test_prefill_long_rows_beyond_staged_page_ids(device, ps):
+    """A row with more pages than a workgroup stages in LDS (2048) takes the
+    global page-id lookup; page size 256 is the reference's default. Both
+    against the oracle."""
+    rng = np.random.default_rng(60 + ps)
+    q_lens = [64, 3, 130] if ps == 4 else [64, 3, 300]
+    prefixes = [9000, 50, 8500] if ps == 4 else [9000, 50, 700]
+    npg = 4600 if ps == 4 else 90
+    kv, indptr, indices, q_indptr = make_rows(rng, q_lens, prefixes, ps, npg)
+    if ps == 4:
+        assert (indptr[1:] - indptr[:-1]).max() > 2048   # the unstaged path runs
+    pool = random_pool(npg, 1, 2, ps, 128, device, 61)
+    q, out = run_prefill(pool, 0, q_lens, kv, indptr, indices, q_indptr, 4, device, 62)
+    want = oracle_prefill(pool, 0, q, q_indptr, indptr, indices, kv)
+    assert max_abs(out, want) <= ATOL
+
+
 def test_prefill_one_token_rows_equal_decode(device):
     """A one-token prefill row is a decode row (use_tensor_cores path)."""
     rng = np.random.default_rng(7)
