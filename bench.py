@@ -10,9 +10,12 @@ token once, plus q, out and page ids) with all inputs resident in HBM.
 
 Also measured: `prefill` — chunked-prefill attention with K/V append (16
 sequences, prompts U[512, 4096], prefixes U[0, 2048], chunk 512) as MFMA
-utilisation of the fp16 dense peak; `gqa_decode` — Llama-3-8B GQA decode
-(32/8 heads, batch 128, contexts U[1024, 8192]) as HBM bandwidth; `remap` —
-the 8192-block remap copy as HBM bandwidth and a Llama-2-70B layer decode
+utilisation of the fp16 dense peak (and `prefill_page256`, the same
+workload on 256-token pages, the reference's default block size);
+`gqa_decode` — Llama-3-8B GQA decode (32/8 heads, batch 128, contexts
+U[1024, 8192]) as HBM bandwidth; `bf16_decode` — the headline decode on a
+bf16 pool (the reference's default dtype); `remap` — the 8192-block remap
+copy as HBM bandwidth and a Llama-2-70B layer decode
 (64/8 heads, batch 256) on the remapped tables, bit-exact against the
 original tables; `pmm` — the Llama-2-7B decode on a pool whose last 784
 pages are 16 dropped Llama-2-7B weight layers (pmm_drop), with the drop and
@@ -89,7 +92,7 @@ def measure_decode(w, pool, layers, args, device, indices_override=None):
                          part_tokens=args.part_tokens)
     ws = torch.zeros(max(plan.workspace_bytes(w.head_dim), 1), dtype=torch.uint8, device=device)
     qs = [torch.randn((w.batch, w.num_qo_heads, w.head_dim), generator=gen, device=device
-                      ).to(torch.float16) for _ in layers]
+                      ).to(pool.k.dtype) for _ in layers]
     out = torch.empty_like(qs[0])
 
     def step(timer=None):
@@ -165,6 +168,30 @@ def bench_gqa(args, device):
         f"part_tokens {res['plan'].info.part_tokens}, group {res['plan'].info.group_size}")
     return {"workload": w.name, "launch_us": res["launch_ms"] * 1e3, "gbs": res["achieved"],
             "hbm_frac": res["achieved"] / HBM_PEAK_GBS, "bytes_per_launch": res["bytes_per_layer"]}
+
+
+def bench_bf16_decode(args, device):
+    """The Llama-2-7B decode workload on a bf16 pool (the reference's default
+    --dtype), 4 layers of the pool swept one launch per layer."""
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+
+    w = workloads.llama2_7b_decode()
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    layers = 4
+    pool = ks.KVPool.allocate(w.num_pages, layers, w.num_kv_heads, w.page_size, w.head_dim,
+                              device, dtype=torch.bfloat16)
+    fill_random_(pool.k, gen)
+    fill_random_(pool.v, gen)
+    res = measure_decode(w, pool, list(range(layers)), args, device)
+    log(f"bf16 decode: {w.name} on a {layers}-layer bf16 pool: per launch "
+        f"{res['launch_ms'] * 1e3:.1f} us = {res['achieved']:.1f} GB/s "
+        f"({res['achieved'] / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
+    out = {"workload": w.name + " (bf16 pool, 4 layers)", "launch_us": res["launch_ms"] * 1e3,
+           "gbs": res["achieved"], "hbm_frac": res["achieved"] / HBM_PEAK_GBS}
+    del pool, res
+    return out
 
 
 def bench_remap(args, device):
@@ -338,11 +365,11 @@ def cpu_baseline(res, budget_s: float) -> dict:
 # ----------------------------------------------------------------- prefill
 
 
-def bench_prefill(args, device):
+def bench_prefill(args, device, page_size=16):
     import kunserve_amd as ks
     from kunserve_amd import workloads
 
-    w = workloads.chunked_prefill()
+    w = workloads.chunked_prefill(page_size=page_size)
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed)
     pool = ks.KVPool.allocate(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device)
@@ -386,12 +413,15 @@ def bench_prefill(args, device):
             if timer:
                 timer.stop(s)
 
-    run_rope()
-    rope_timer = LaunchTimer()
-    run_rope(rope_timer)
-    rope_ms = rope_timer.mean_ms() * len(steps)
-    log(f"rope + append prologue: {rope_ms:.3f} ms for the 8 steps = "
-        f"{rope_bytes / (rope_ms * 1e-3) / 1e9:.1f} GB/s")
+    rope = None
+    if page_size == 16:
+        run_rope()
+        rope_timer = LaunchTimer()
+        run_rope(rope_timer)
+        rope_ms = rope_timer.mean_ms() * len(steps)
+        log(f"rope + append prologue: {rope_ms:.3f} ms for the 8 steps = "
+            f"{rope_bytes / (rope_ms * 1e-3) / 1e9:.1f} GB/s")
+        rope = {"ms": rope_ms, "bytes": rope_bytes, "gbs": rope_bytes / (rope_ms * 1e-3) / 1e9}
 
     reps = max(1, args.steps // 4)
     for _ in range(max(1, args.warmup)):
@@ -409,14 +439,13 @@ def bench_prefill(args, device):
     log("prefill per-step attention ms: " + ", ".join(f"{t:.3f}" for t in per_step))
     flops = w.causal_flops()
     tflops = flops / (attn_ms * 1e-3) / 1e12
-    log(f"prefill: {len(steps)} chunk steps, {elapsed * 1e3:.3f} ms with append; attention "
+    log(f"prefill (page {page_size}): {len(steps)} chunk steps, {elapsed * 1e3:.3f} ms with append; attention "
         f"{attn_ms:.3f} ms = {tflops:.1f} TFLOP/s ({tflops / FP16_MFMA_PEAK_TFLOPS * 100:.1f}% "
         f"of fp16 MFMA peak)")
     return {"workload": w.name, "causal_tflop": flops / 1e12, "steps": len(steps),
             "ms_with_append": elapsed * 1e3, "attention_ms": attn_ms, "tflops": tflops,
-            "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS,
-            "rope_append": {"ms": rope_ms, "bytes": rope_bytes,
-                            "gbs": rope_bytes / (rope_ms * 1e-3) / 1e9}}
+            "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS, "page_size": page_size,
+            "rope_append": rope}
 
 
 # -------------------------------------------------------------------- swap
@@ -501,7 +530,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
-    ap.add_argument("--only", choices=["decode", "prefill", "gqa", "remap", "pmm", "swap"],
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill256", "gqa", "bf16", "remap",
+                                       "pmm", "swap"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
@@ -524,8 +554,14 @@ def main():
     if args.only == "prefill":
         print(json.dumps({"prefill": bench_prefill(args, device)}))
         return
+    if args.only == "prefill256":
+        print(json.dumps({"prefill_page256": bench_prefill(args, device, page_size=256)}))
+        return
     if args.only == "gqa":
         print(json.dumps({"gqa_decode": bench_gqa(args, device)}))
+        return
+    if args.only == "bf16":
+        print(json.dumps({"bf16_decode": bench_bf16_decode(args, device)}))
         return
     if args.only == "remap":
         print(json.dumps({"remap": bench_remap(args, device)}))
@@ -550,11 +586,15 @@ def main():
     w = dec["workload"]
     del dec["pool"], dec["qs"]
     torch.cuda.empty_cache()
-    prefill = gqa = remap = pmm = swp = None
+    prefill = prefill256 = gqa = bf16 = remap = pmm = swp = None
     if args.only is None:
         prefill = bench_prefill(args, device)
         torch.cuda.empty_cache()
+        prefill256 = bench_prefill(args, device, page_size=256)
+        torch.cuda.empty_cache()
         gqa = bench_gqa(args, device)
+        torch.cuda.empty_cache()
+        bf16 = bench_bf16_decode(args, device)
         torch.cuda.empty_cache()
         remap = bench_remap(args, device)
         torch.cuda.empty_cache()
@@ -597,7 +637,9 @@ def main():
         },
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "prefill_page256": prefill256,
         "gqa_decode": gqa,
+        "bf16_decode": bf16,
         "remap": remap,
         "pmm": pmm,
         "swap": swp,

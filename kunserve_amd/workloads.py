@@ -130,15 +130,21 @@ class PrefillShape:
         return 4 * self.num_qo_heads * self.head_dim * total
 
 
-def chunked_prefill(seed: int = 1004, num_pages: int = 8192) -> PrefillShape:
+def chunked_prefill(seed: int = 1004, num_pages: int | None = None,
+                    page_size: int = 16) -> PrefillShape:
     """16 sequences, prompts U[512, 4096], prefixes U[0, 2048] already in
-    pages, chunk 512, Llama-2-7B heads (32/32, head_dim 128), page 16."""
+    pages, chunk 512, Llama-2-7B heads (32/32, head_dim 128), page 16 (or
+    page_size; the pool holds the same 131072 tokens by default)."""
     rng = np.random.default_rng(seed)
     prompt = rng.integers(512, 4097, size=16).astype(np.int32)
     prefix = rng.integers(0, 2049, size=16).astype(np.int32)
-    pages = _tables(rng, prompt + prefix, 16, num_pages)
-    return PrefillShape("chunked prefill 16 seqs prompt512-4096 prefix0-2048 chunk512", 32, 32,
-                        128, 16, num_pages, prompt, prefix, 512, pages, seed)
+    if num_pages is None:
+        num_pages = 8192 * 16 // page_size
+    pages = _tables(rng, prompt + prefix, page_size, num_pages)
+    name = "chunked prefill 16 seqs prompt512-4096 prefix0-2048 chunk512"
+    if page_size != 16:
+        name += f" page{page_size}"
+    return PrefillShape(name, 32, 32, 128, page_size, num_pages, prompt, prefix, 512, pages, seed)
 
 
 @dataclass
