@@ -183,3 +183,53 @@ def test_swap_rejects_out_of_range_ids_before_any_copy():
         _lib.call("kunserve_swap_blocks", src.ctypes.data, dst.ctypes.data, 2, 0, dummy, dummy,
                   4, dummy, dummy, 8, 1024, None)
     assert e.value.code == _lib.ERANGE
+
+
+# ------------------------------------------------------------------------
+# Randomised plan properties (hypothesis): the coverage invariants above on
+# arbitrary batches, head layouts, CU counts and partition sizes.
+
+from hypothesis import HealthCheck, given, settings, strategies as st  # noqa: E402
+
+HEADS = [(1, 1), (4, 4), (8, 2), (12, 4), (32, 8), (64, 8), (32, 32), (6, 2)]
+
+
+@settings(max_examples=60, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@given(kv=st.lists(st.integers(0, 20000), min_size=0, max_size=24),
+       heads=st.sampled_from(HEADS),
+       num_cus=st.sampled_from([0, 1, 64, 256, 1024]),
+       part=st.sampled_from([0, 256, 320, 512, 1024, 4096]))
+def test_decode_plan_properties(kv, heads, num_cus, part):
+    hq, hkv = heads
+    kv = np.asarray(kv, dtype=np.int32)
+    cap = _lib.lib().kunserve_decode_plan_bound(kv.ctypes.data if kv.size else None, kv.size)
+    buf = np.zeros(max(cap, 1), dtype=np.int32)
+    info = _lib.DecodePlanInfo()
+    _lib.call("kunserve_decode_plan", kv.ctypes.data if kv.size else None, kv.size, hq, hkv,
+              num_cus, part, buf.ctypes.data, cap, ctypes.byref(info))
+    work = buf[:4 * info.num_work].reshape(-1, 4)
+    merges = buf[4 * info.num_work:info.plan_ints].reshape(-1, 4)
+    assert part == 0 or info.part_tokens == part
+    covered = np.zeros(kv.size, dtype=np.int64)
+    for seq, b, e, slot in work:
+        assert 0 <= b <= e <= kv[seq] and e - b <= info.part_tokens
+        covered[seq] += e - b
+    assert np.array_equal(covered, kv)
+    assert np.all(np.diff(work[:, 2] - work[:, 1]) <= 0)
+    assert sorted(work[work[:, 3] >= 0, 3].tolist()) == list(range(info.num_slots))
+    for seq, s0, n, _ in merges:
+        assert n > 1 and sorted(work[work[:, 0] == seq, 3].tolist()) == list(range(s0, s0 + n))
+
+
+@settings(max_examples=60, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@given(rows=st.lists(st.tuples(st.integers(0, 1500), st.integers(0, 5000)), min_size=1,
+                     max_size=12),
+       heads=st.sampled_from(HEADS),
+       num_cus=st.sampled_from([0, 1, 64, 256, 1024]))
+def test_prefill_plan_properties(rows, heads, num_cus):
+    hq, hkv = heads
+    q_lens = np.array([q for q, _ in rows], dtype=np.int64)
+    kv = np.array([q + p for q, p in rows], dtype=np.int32)
+    q_indptr = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    info, items, merges = _prefill_plan(q_indptr, kv, hq, hkv, num_cus)
+    _check_prefill_plan(q_indptr, q_lens, kv, hq, hkv, info, items, merges)
