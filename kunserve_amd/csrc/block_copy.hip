@@ -260,6 +260,9 @@ struct SwapIdSlot {
   bool busy = false;   // handed out, event not yet recorded
 };
 constexpr size_t kMaxSwapSlots = 64;
+// Ids a slot holds at least (src and dst of 8192 blocks, 64 KiB): slots
+// are rarely regrown, and a regrowth frees a completed slot's buffer only.
+constexpr int64_t kMinSwapSlotIds = 16384;
 std::mutex g_swap_mu;
 std::vector<SwapIdSlot> g_swap_slots;
 uint64_t g_swap_clock = 0;
@@ -301,7 +304,7 @@ int acquire_swap_ids(int64_t count, hipStream_t s, int32_t** out) {
     if (pick->ids) KSV_CHECK_HIP(hipHostFree(pick->ids));
     pick->ids = nullptr;
     pick->cap = 0;
-    const int64_t cap = std::max<int64_t>(count, 4096);
+    const int64_t cap = std::max<int64_t>(count, kMinSwapSlotIds);
     KSV_CHECK_HIP(hipHostMalloc(reinterpret_cast<void**>(&pick->ids), cap * sizeof(int32_t),
                                 hipHostMallocDefault));
     pick->cap = cap;
