@@ -8,7 +8,8 @@ import torch
 from kunserve_amd import DecodePlan, paged_decode, workloads
 from oracle import paged_attention_ref as ref
 
-from helpers import ATOL, compact_for_oracle, max_abs, random_pool, random_tensor, table_from_csr
+from helpers import (ATOL, ATOL_BF16, compact_for_oracle, max_abs, random_pool, random_tensor,
+                     table_from_csr, to_numpy)
 
 pytestmark = pytest.mark.gpu
 
@@ -27,7 +28,7 @@ def oracle_decode(pool, layer, indptr, indices, kv_len, q, rows=None):
     rows = np.arange(len(kv_len)) if rows is None else np.asarray(rows)
     k, v, ip, ix = compact_for_oracle(pool, 0 if pool.num_layers == 1 else layer, indptr,
                                       indices, rows)
-    qn = q[torch.from_numpy(rows).to(q.device)].cpu().numpy()
+    qn = to_numpy(q[torch.from_numpy(rows).to(q.device)])
     return ref.decode_attention(qn, k, v, 0, ip, ix, np.asarray(kv_len)[rows],
                                 1.0 / math.sqrt(pool.head_dim))
 
@@ -182,3 +183,92 @@ def test_llama2_70b_decode_on_remapped_tables(device):
     rows = np.unique(np.concatenate([order[:2], order[-2:], order[::64]]))
     want = oracle_decode(pool, 5, ip2, ix2, w2.kv_len, q, rows)
     assert max_abs(out2[torch.from_numpy(rows).to(device)], want) <= ATOL
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 4)])
+@pytest.mark.parametrize("num_cus", [3, 256])
+def test_decode_plans_agree_with_each_other_and_the_oracle(device, dtype, head_dim, hq, hkv,
+                                                           num_cus):
+    """The automatic plan (long partitions when few CUs are assumed) and a
+    fixed 512-token plan agree with the oracle and each other, in fp16 and
+    bf16, with zero-length rows and rows from 1 to 9000 tokens."""
+    rng = np.random.default_rng(head_dim + 10 * hq + hkv + num_cus)
+    kv = np.array([0, 1, 5, 64, 65, 300, 1023, 4100, 9000, 17, 0, 2500], dtype=np.int32)
+    need = (kv + 15) // 16
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    npg = int(indptr[-1]) + 3
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, hkv, 16, head_dim, device, 71, dtype=dtype)
+    table = table_from_csr(indptr, indices, kv, device)
+    q = random_tensor((len(kv), hq, head_dim), device, 72, dtype=dtype)
+    auto = DecodePlan(kv, hq, hkv, device, num_cus=num_cus)
+    fixed = DecodePlan(kv, hq, hkv, device, part_tokens=512, num_cus=num_cus)
+    assert fixed.info.num_merge > 0
+    out_a = paged_decode(pool, 0, table, q, auto).float()
+    out_f = paged_decode(pool, 0, table, q, fixed).float()
+    torch.cuda.synchronize()
+    want = oracle_decode(pool, 0, indptr, indices, kv, q)
+    tol = ATOL if dtype == torch.float16 else ATOL_BF16
+    assert max_abs(out_a, want) <= tol
+    assert max_abs(out_f, want) <= tol
+    assert max_abs(out_a, out_f) <= tol
+    assert torch.all(out_a[0] == 0) and torch.all(out_a[10] == 0)
+
+
+def _small_decode_case(device, seed=81):
+    rng = np.random.default_rng(seed)
+    kv = rng.integers(1, 3000, 40).astype(np.int32)
+    need = (kv + 15) // 16
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    npg = int(indptr[-1]) + 9
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, 8, 16, 128, device, seed)
+    table = table_from_csr(indptr, indices, kv, device)
+    q = random_tensor((len(kv), 8, 128), device, seed + 1)
+    plan = DecodePlan(kv, 8, 8, device, part_tokens=256)
+    return pool, table, q, plan, (indptr, indices, kv)
+
+
+def test_decode_is_deterministic_over_many_launches_and_streams(device):
+    """600 launches in a row, then launches on a second stream, give the
+    bits of the first launch every time (no state carried between
+    launches)."""
+    pool, table, q, plan, (indptr, indices, kv) = _small_decode_case(device)
+    ws = torch.empty(max(plan.workspace_bytes(128), 1), dtype=torch.uint8, device=device)
+    first = paged_decode(pool, 0, table, q, plan, workspace=ws).clone()
+    torch.cuda.synchronize()
+    want = oracle_decode(pool, 0, indptr, indices, kv, q)
+    assert max_abs(first, want) <= ATOL
+    out = torch.empty_like(first)
+    for i in range(600):
+        paged_decode(pool, 0, table, q, plan, out=out, workspace=ws)
+        if i % 100 == 99:
+            torch.cuda.synchronize()
+            assert torch.equal(out, first), f"launch {i}"
+    s2 = torch.cuda.Stream(device)
+    with torch.cuda.stream(s2):
+        outs = [paged_decode(pool, 0, table, q, plan) for _ in range(4)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, first) for o in outs)
+
+
+def test_decode_graph_replays(device):
+    """A decode launch captured in a HIP graph gives the eager result on
+    every replay, with eager work and synchronisation between replays."""
+    pool, table, q, plan, _ = _small_decode_case(device, 91)
+    ws = torch.empty(max(plan.workspace_bytes(128), 1), dtype=torch.uint8, device=device)
+    out = torch.empty_like(q)
+    eager = paged_decode(pool, 0, table, q, plan, workspace=ws).clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        paged_decode(pool, 0, table, q, plan, out=out, workspace=ws)
+    for r in range(5):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"
+        paged_decode(pool, 0, table, q, plan, workspace=ws)   # eager launch between replays
+        torch.cuda.synchronize()
