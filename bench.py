@@ -95,12 +95,9 @@ def measure_decode(w, pool, layers, args, device, indices_override=None):
                       ).to(pool.k.dtype) for _ in layers]
     out = torch.empty_like(qs[0])
 
-    def step(timer=None):
+    def step():
         for i, layer in enumerate(layers):
-            s = timer.start() if timer else None
             ks.paged_decode(pool, layer, table, qs[i], plan, out=out, workspace=ws)
-            if timer:
-                timer.stop(s)
 
     for _ in range(args.warmup):
         step()
@@ -110,12 +107,18 @@ def measure_decode(w, pool, layers, args, device, indices_override=None):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    # Per-launch durations from HIP events on the launch stream (separate
-    # pass over the same steps so the events do not perturb the headline).
-    timer = LaunchTimer()
+    # Per-launch duration from HIP events on the launch stream around a
+    # second pass over the same steps, divided by the launches in it.
+    # Events around every launch would add their own packets (about 5 us
+    # per launch) to what they measure.
+    stream = torch.cuda.current_stream(device)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
     for _ in range(args.steps):
-        step(timer)
-    launch_ms = timer.mean_ms()
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    launch_ms = ev0.elapsed_time(ev1) / (args.steps * len(layers))
     bytes_per_layer = w.kv_bytes_per_layer()
     return {
         "value": bytes_per_layer * len(layers) * args.steps / elapsed / 1e9,
