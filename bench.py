@@ -53,6 +53,20 @@ def fill_random_(t: torch.Tensor, gen: torch.Generator, slab_dim: int = 1) -> No
         s.copy_(torch.randn(s.shape, generator=gen, device=t.device, dtype=torch.float32))
 
 
+def region_ms(fn, device) -> float:
+    """Milliseconds of GPU time of `fn()` (which enqueues work on the
+    current stream): HIP events on that stream before and after it. One
+    event pair around a whole pass leaves out the packets that events
+    around every launch add (about 5 us per launch)."""
+    stream = torch.cuda.current_stream(device)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    fn()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1)
+
+
 class LaunchTimer:
     """HIP events around each launch on the current stream."""
 
@@ -111,14 +125,11 @@ def measure_decode(w, pool, layers, args, device, indices_override=None):
     # second pass over the same steps, divided by the launches in it.
     # Events around every launch would add their own packets (about 5 us
     # per launch) to what they measure.
-    stream = torch.cuda.current_stream(device)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(args.steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    launch_ms = ev0.elapsed_time(ev1) / (args.steps * len(layers))
+    def timed_pass():
+        for _ in range(args.steps):
+            step()
+
+    launch_ms = region_ms(timed_pass, device) / (args.steps * len(layers))
     bytes_per_layer = w.kv_bytes_per_layer()
     return {
         "value": bytes_per_layer * len(layers) * args.steps / elapsed / 1e9,
@@ -218,12 +229,8 @@ def bench_remap(args, device):
     reps = max(2, args.steps // 4)
     ks.copy_blocks(pool, src, dst)
     torch.cuda.synchronize()
-    timer = LaunchTimer()
-    for _ in range(reps):
-        s = timer.start()
-        ks.copy_blocks(pool, src, dst)
-        timer.stop(s)
-    copy_ms = timer.mean_ms()
+    copy_ms = region_ms(lambda: [ks.copy_blocks(pool, src, dst) for _ in range(reps)],
+                        device) / reps
     copy_gbs = r.copy_bytes() / (copy_ms * 1e-3) / 1e9
     log(f"block copy: {len(r.src)} blocks of {r.copy_bytes() / 4 / len(r.src) / 2**20:.0f} MiB "
         f"(K and V), {copy_ms:.3f} ms = {copy_gbs:.1f} GB/s "
@@ -409,19 +416,15 @@ def bench_prefill(args, device, page_size=16):
         T = q.shape[0]
         rope_bytes += 2 * T * w.num_qo_heads * w.head_dim * 2 + 4 * T * w.num_kv_heads * w.head_dim * 2
 
-    def run_rope(timer=None):
+    def run_rope():
         for table, qi, plan, q, k, v, out in steps:
-            s = timer.start() if timer else None
             ks.rope_append_kv(pool, 0, table, qi, q, k, v, inv_freq)
-            if timer:
-                timer.stop(s)
 
     rope = None
     if page_size == 16:
         run_rope()
-        rope_timer = LaunchTimer()
-        run_rope(rope_timer)
-        rope_ms = rope_timer.mean_ms() * len(steps)
+        rope_reps = 4
+        rope_ms = region_ms(lambda: [run_rope() for _ in range(rope_reps)], device) / rope_reps
         log(f"rope + append prologue: {rope_ms:.3f} ms for the 8 steps = "
             f"{rope_bytes / (rope_ms * 1e-3) / 1e9:.1f} GB/s")
         rope = {"ms": rope_ms, "bytes": rope_bytes, "gbs": rope_bytes / (rope_ms * 1e-3) / 1e9}
@@ -435,9 +438,16 @@ def bench_prefill(args, device, page_size=16):
         run()
     torch.cuda.synchronize()
     elapsed = (time.perf_counter() - t0) / reps
-    timer = LaunchTimer()
+
+    def run_attention():
+        for table, qi, plan, q, k, v, out in steps:
+            ks.paged_prefill(pool, 0, table, qi, q, plan, out=out)
+
+    # Attention alone (the steps' K/V are in the pages from the runs above).
+    attn_ms = region_ms(lambda: [run_attention() for _ in range(reps)], device) / reps
+    timer = LaunchTimer()   # per-step breakdown (these events add about 5 us a step)
     run(timer)
-    attn_ms = timer.mean_ms() * len(steps)
+    torch.cuda.synchronize()
     per_step = [a.elapsed_time(b) for a, b in timer.pairs]
     log("prefill per-step attention ms: " + ", ".join(f"{t:.3f}" for t in per_step))
     flops = w.causal_flops()
