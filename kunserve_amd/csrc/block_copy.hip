@@ -362,7 +362,8 @@ extern "C" int kunserve_swap_blocks(const int64_t* src_ids_host, const int64_t* 
   const bool mapped = hipHostGetDevicePointer(&k_host_dev, k_swap_host, 0) == hipSuccess &&
                       hipHostGetDevicePointer(&v_host_dev, v_swap_host, 0) == hipSuccess &&
                       k_host_dev && v_host_dev;
-  if (mapped) {
+  // The copy kernel takes block ids as int32.
+  if (mapped && src_limit <= INT32_MAX && dst_limit <= INT32_MAX) {
     (void)hipGetLastError();
     int32_t* ids = nullptr;
     int rc = acquire_swap_ids(2 * n, s, &ids);
