@@ -1,8 +1,9 @@
 """CPU oracle of the paged-KV attention path — TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this module, and only as the checker or the timed CPU baseline; the
-product path (kunserve_amd) never calls it.
+import this module, and only as the reference that GPU results are compared
+against or as the timed CPU baseline; the product path (kunserve_amd) never
+calls it.
 
 The reference's kernels (FlashTransformer, with FlashInfer / flash-attention
 underneath) are not present in the reference tree (empty git submodule,

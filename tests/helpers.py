@@ -1,4 +1,4 @@
-"""Shared helpers of the GPU parity tests (checkers only)."""
+"""Shared helpers of the GPU parity tests (test code only)."""
 from __future__ import annotations
 
 import numpy as np
