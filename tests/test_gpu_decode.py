@@ -272,3 +272,58 @@ def test_decode_graph_replays(device):
         assert torch.equal(out, eager), f"replay {r}"
         paged_decode(pool, 0, table, q, plan, workspace=ws)   # eager launch between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("ratio", [4, 8])
+def test_gqa_decode_equals_mha_on_repeated_heads(device, ratio):
+    """GQA decode (the MFMA kernel for 4 and 8 q heads per KV head) equals
+    MHA decode (the VALU kernel) on a pool whose KV heads are repeated
+    `ratio` times, each q head reading its own copy."""
+    from kunserve_amd import KVPool
+    rng = np.random.default_rng(ratio)
+    hkv, hq = 4, 4 * ratio
+    kv = np.array([1, 33, 700, 2049, 5000, 16], dtype=np.int32)
+    need = (kv + 15) // 16
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    npg = int(indptr[-1]) + 4
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, hkv, 16, 128, device, 111)
+    mha = KVPool(pool.k.repeat_interleave(ratio, dim=2).contiguous(),
+                 pool.v.repeat_interleave(ratio, dim=2).contiguous())
+    table = table_from_csr(indptr, indices, kv, device)
+    q = random_tensor((len(kv), hq, 128), device, 112)
+    gqa_plan = DecodePlan(kv, hq, hkv, device)
+    mha_plan = DecodePlan(kv, hq, hq, device)
+    assert gqa_plan.info.group_size == min(ratio, 8) and mha_plan.info.group_size == 1
+    out_g = paged_decode(pool, 0, table, q, gqa_plan).float()
+    out_m = paged_decode(mha, 0, table, q, mha_plan).float()
+    torch.cuda.synchronize()
+    assert max_abs(out_g, out_m) <= ATOL
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (32, 4)])
+def test_decode_closed_forms(device, hq, hkv):
+    """One cached token gives its V row exactly; q = 0 gives the mean of the
+    row's V (uniform weights), on the VALU (G = 1) and MFMA (G = 8) kernels."""
+    rng = np.random.default_rng(hq + hkv)
+    kv = np.array([1, 1, 300, 4097], dtype=np.int32)
+    need = (kv + 15) // 16
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    npg = int(indptr[-1]) + 2
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, hkv, 16, 128, device, 121)
+    table = table_from_csr(indptr, indices, kv, device)
+    plan = DecodePlan(kv, hq, hkv, device, part_tokens=1024)
+    q = random_tensor((len(kv), hq, 128), device, 122)
+    q[2:] = 0
+    out = paged_decode(pool, 0, table, q, plan)
+    torch.cuda.synchronize()
+    ratio = hq // hkv
+    for b in (0, 1):
+        v0 = pool.v[int(indices[indptr[b]]), 0, :, 0]            # [hkv, D]
+        assert torch.equal(out[b], v0.repeat_interleave(ratio, dim=0))
+    for b in (2, 3):
+        pages = torch.from_numpy(indices[indptr[b]:indptr[b + 1]].astype(np.int64)).to(device)
+        rows = pool.v[pages, 0].permute(1, 0, 2, 3).reshape(hkv, -1, 128)[:, :int(kv[b])]
+        mean = rows.float().mean(dim=1).repeat_interleave(ratio, dim=0)
+        assert max_abs(out[b].float(), mean) <= ATOL
