@@ -14,7 +14,8 @@ utilisation of the fp16 dense peak (and `prefill_page256`, the same
 workload on 256-token pages, the reference's default block size);
 `gqa_decode` — Llama-3-8B GQA decode (32/8 heads, batch 128, contexts
 U[1024, 8192]) as HBM bandwidth; `bf16_decode` — the headline decode on a
-bf16 pool (the reference's default dtype); `remap` — the 8192-block remap
+bf16 pool (the reference's default dtype), and `bf16_decode_page256` on a
+bf16 pool of 256-token pages (both reference defaults); `remap` — the 8192-block remap
 copy as HBM bandwidth and a Llama-2-70B layer decode
 (64/8 heads, batch 256) on the remapped tables, bit-exact against the
 original tables; `pmm` — the Llama-2-7B decode on a pool whose last 784
@@ -184,13 +185,14 @@ def bench_gqa(args, device):
             "hbm_frac": res["achieved"] / HBM_PEAK_GBS, "bytes_per_launch": res["bytes_per_layer"]}
 
 
-def bench_bf16_decode(args, device):
+def bench_bf16_decode(args, device, page_size=16):
     """The Llama-2-7B decode workload on a bf16 pool (the reference's default
-    --dtype), 4 layers of the pool swept one launch per layer."""
+    --dtype), 4 layers of the pool swept one launch per layer; page_size 256
+    is the reference's default block size as well."""
     import kunserve_amd as ks
     from kunserve_amd import workloads
 
-    w = workloads.llama2_7b_decode()
+    w = workloads.llama2_7b_decode(page_size=page_size)
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed)
     layers = 4
@@ -543,8 +545,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill256", "gqa", "bf16", "remap",
-                                       "pmm", "swap"],
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill256", "gqa", "bf16",
+                                       "bf16p256", "remap", "pmm", "swap"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
@@ -576,6 +578,9 @@ def main():
     if args.only == "bf16":
         print(json.dumps({"bf16_decode": bench_bf16_decode(args, device)}))
         return
+    if args.only == "bf16p256":
+        print(json.dumps({"bf16_decode_page256": bench_bf16_decode(args, device, page_size=256)}))
+        return
     if args.only == "remap":
         print(json.dumps({"remap": bench_remap(args, device)}))
         return
@@ -599,7 +604,7 @@ def main():
     w = dec["workload"]
     del dec["pool"], dec["qs"]
     torch.cuda.empty_cache()
-    prefill = prefill256 = gqa = bf16 = remap = pmm = swp = None
+    prefill = prefill256 = gqa = bf16 = bf16_256 = remap = pmm = swp = None
     if args.only is None:
         prefill = bench_prefill(args, device)
         torch.cuda.empty_cache()
@@ -608,6 +613,8 @@ def main():
         gqa = bench_gqa(args, device)
         torch.cuda.empty_cache()
         bf16 = bench_bf16_decode(args, device)
+        torch.cuda.empty_cache()
+        bf16_256 = bench_bf16_decode(args, device, page_size=256)
         torch.cuda.empty_cache()
         remap = bench_remap(args, device)
         torch.cuda.empty_cache()
@@ -653,6 +660,7 @@ def main():
         "prefill_page256": prefill256,
         "gqa_decode": gqa,
         "bf16_decode": bf16,
+        "bf16_decode_page256": bf16_256,
         "remap": remap,
         "pmm": pmm,
         "swap": swp,

@@ -71,14 +71,19 @@ def single_layer_decode(seed: int = 1001) -> DecodeShape:
                        _tables(rng, kv, 16, 512), seed)
 
 
-def llama2_7b_decode(seed: int = 1002) -> DecodeShape:
-    """Llama-2-7B decode: 32 layers, 32/32 heads, head_dim 128, page 16,
-    16384-page pool, batch 64, contexts round(lognormal(ln 700, 1.0))
+def llama2_7b_decode(seed: int = 1002, page_size: int = 16) -> DecodeShape:
+    """Llama-2-7B decode: 32 layers, 32/32 heads, head_dim 128, a pool of
+    262144 tokens (16384 pages of 16, or 1024 of 256: the reference's
+    default block size), batch 64, contexts round(lognormal(ln 700, 1.0))
     clipped to [16, 4096]."""
     rng = np.random.default_rng(seed)
     kv = np.clip(np.round(rng.lognormal(np.log(700.0), 1.0, size=64)), 16, 4096).astype(np.int32)
-    return DecodeShape("llama2-7b decode b64 ctx lognormal(700) x32 layers", 32, 32, 32, 128, 16,
-                       16384, kv, _tables(rng, kv, 16, 16384), seed)
+    num_pages = 16384 * 16 // page_size
+    name = "llama2-7b decode b64 ctx lognormal(700) x32 layers"
+    if page_size != 16:
+        name += f" page{page_size}"
+    return DecodeShape(name, 32, 32, 32, 128, page_size, num_pages, kv,
+                       _tables(rng, kv, page_size, num_pages), seed)
 
 
 def llama3_8b_gqa_decode(seed: int = 1003) -> DecodeShape:

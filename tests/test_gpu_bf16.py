@@ -124,3 +124,23 @@ def test_bf16_llama_op_mixed_step(device):
     want = ref.prefill_attention(to_numpy(q), q_indptr, k_pool0, v_pool0, 1, indptr, indices, kv,
                                  1 / math.sqrt(128))
     assert out.dtype == BF16 and max_abs(out, want) <= ATOL_BF16
+
+
+def test_bf16_decode_on_256_token_pages(device):
+    """The reference's default configuration: bf16 pool, 256-token pages,
+    rows that end inside a page and rows longer than one partition."""
+    rng = np.random.default_rng(256)
+    kv = np.array([1, 255, 256, 257, 3000, 9000], dtype=np.int32)
+    need = (kv + 255) // 256
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    npg = int(indptr[-1]) + 3
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, 8, 256, 128, device, 257, dtype=BF16)
+    table = table_from_csr(indptr, indices, kv, device)
+    q = random_tensor((len(kv), 8, 128), device, 258, dtype=BF16)
+    plan = DecodePlan(kv, 8, 8, device, part_tokens=512)
+    out = paged_decode(pool, 0, table, q, plan)
+    torch.cuda.synchronize()
+    k, v, ip, ix = compact_for_oracle(pool, 0, indptr, indices, np.arange(len(kv)))
+    want = ref.decode_attention(to_numpy(q), k, v, 0, ip, ix, kv, 1.0 / math.sqrt(128))
+    assert max_abs(out, want) <= ATOL_BF16

@@ -38,7 +38,8 @@ def test_csr_truncates_and_validates():
 
 def test_workloads_are_seeded_and_disjoint():
     for make in (workloads.single_layer_decode, workloads.llama2_7b_decode,
-                 workloads.llama3_8b_gqa_decode):
+                 workloads.llama3_8b_gqa_decode,
+                 lambda: workloads.llama2_7b_decode(page_size=256)):
         a, b = make(), make()
         assert np.array_equal(a.kv_len, b.kv_len)
         indptr, indices = a.csr()
@@ -46,6 +47,8 @@ def test_workloads_are_seeded_and_disjoint():
         assert indices.max() < a.num_pages
         assert np.array_equal(np.diff(indptr), (a.kv_len + a.page_size - 1) // a.page_size)
     w = workloads.llama2_7b_decode()
+    w256 = workloads.llama2_7b_decode(page_size=256)
+    assert np.array_equal(w.kv_len, w256.kv_len) and w256.num_pages * 256 == w.num_pages * 16
     assert w.kv_len.min() >= 16 and w.kv_len.max() <= 4096
     # sample median of 64 lognormal(ln 700, 1) draws: 700 within a few standard errors
     assert 450 <= np.median(w.kv_len) <= 1100
