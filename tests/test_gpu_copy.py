@@ -107,6 +107,43 @@ def test_swap_out_and_in_round_trip(device):
     assert not k2[:11].view(torch.int16).any()
 
 
+def test_swap_through_the_abi_with_pageable_host_pools(device):
+    """Host pools the device cannot map (plain pageable memory) take the
+    fallback: one DMA copy per run of consecutive ids, both directions."""
+    import ctypes
+    from kunserve_amd import _lib
+    shape = (12, 2, 2, 16, 64)
+    k = unique_pool(shape, device)
+    v = unique_pool(shape, device, 5)
+    block_bytes = int(np.prod(shape[1:])) * 2
+    kh = np.zeros((8,) + shape[1:], dtype=np.int16)
+    vh = np.zeros((8,) + shape[1:], dtype=np.int16)
+    stream = torch.cuda.current_stream(device).cuda_stream
+
+    def call(src, dst, is_in, n_dev, n_host):
+        s = np.asarray(src, dtype=np.int64)
+        d = np.asarray(dst, dtype=np.int64)
+        _lib.call("kunserve_swap_blocks", s.ctypes.data, d.ctypes.data, len(s), int(is_in),
+                  k.data_ptr(), v.data_ptr(), n_dev, kh.ctypes.data, vh.ctypes.data, n_host,
+                  block_bytes, stream)
+        torch.cuda.synchronize()
+
+    src, dst = [3, 4, 5, 9, 0], [0, 1, 2, 6, 7]   # a run of three, then two singles
+    call(src, dst, False, 12, 8)
+    want_k = np.zeros_like(kh)
+    want_v = np.zeros_like(vh)
+    ref.swap(src, dst, k.view(torch.int16).cpu().numpy(), want_k)
+    ref.swap(src, dst, v.view(torch.int16).cpu().numpy(), want_v)
+    assert np.array_equal(kh, want_k) and np.array_equal(vh, want_v)
+    k_before = k.view(torch.int16).cpu().numpy()
+    call([0, 1, 2, 7], [10, 11, 8, 4], True, 12, 8)
+    want = k_before.copy()
+    ref.swap([0, 1, 2, 7], [10, 11, 8, 4], kh, want)
+    assert np.array_equal(k.view(torch.int16).cpu().numpy(), want)
+    with pytest.raises(_lib.KunserveError):
+        call([8], [0], True, 12, 8)   # host block 8 is outside [0, 8)
+
+
 def test_swap_on_side_stream_is_ordered(device):
     shape = (4, 1, 2, 16, 64)
     k = unique_pool(shape, device)
