@@ -6,9 +6,9 @@
 // Design for gfx950 (wave64, 256 CUs):
 //  * The host plan cuts every sequence into partitions of part_tokens and
 //    orders them longest first; the grid is work items x head groups, each
-//    XCD running all head groups of every 8th item, so mixed context
-//    lengths still give an even, device-filling grid that is dispatched
-//    longest item first on every XCD.
+//    XCD running all head groups of one item in every 8 (alternating
+//    direction), so mixed context lengths still give an even,
+//    device-filling grid that is dispatched longest item first on every XCD.
 //  * A workgroup (4 waves) owns one partition of one KV head and all
 //    `G` query heads that share it (GQA: one KV read serves G heads).
 //  * The partition's slice of the page table is staged in LDS once; after
@@ -66,18 +66,19 @@ struct DecodeArgs {
 };
 
 // Work item and head group of workgroup b. The hardware hands workgroup b
-// to XCD b % 8; XCD x runs every head group of items x, x + 8, x + 16, ...
-// in the plan's longest-first order. The pages an XCD reads at a time are
-// then those of its own few items (measured 1-2% faster than spreading
-// each item's head groups over all XCDs), and every XCD still gets a
-// stride-8 sample of the sorted items. Returns false for the grid's
-// padding workgroups (the grid is 8 * ceil(items / 8) * head_groups).
+// to XCD b % 8; XCD x runs every head group of one item of each group of
+// 8 consecutive items of the plan's longest-first order: item 8r + x for
+// even r and 8r + 7 - x for odd r, so no XCD always gets the longest of
+// the 8. The pages an XCD reads at a time are then those of its own few
+// items (measured 1-2% faster than spreading each item's head groups over
+// all XCDs). Returns false for the grid's padding workgroups (the grid is
+// 8 * ceil(items / 8) * head_groups).
 __device__ __forceinline__ bool decode_work(const DecodeArgs& a, int& item, int& hg) {
   const int b = int(blockIdx.x);
   const int j = b >> 3;
   const int local = j / a.head_groups;
   hg = j - local * a.head_groups;
-  item = (b & 7) + 8 * local;
+  item = 8 * local + ((local & 1) ? 7 - (b & 7) : (b & 7));
   return item < a.num_work;
 }
 
