@@ -144,8 +144,8 @@ def test_prefill_plan_covers_every_tile_once(hq, hkv, n):
 @pytest.mark.parametrize("num_cus", [0, 64, 256, 1024])
 def test_prefill_plan_splits_small_steps(num_cus):
     """A step with fewer q-tile items than CUs (one long row: the last step
-    of a chunked prefill, 64 items) is split over about 2 x CUs workgroups;
-    a step with enough items is not."""
+    of a chunked prefill, 64 items) is split over about one workgroup per
+    CU; a step with enough items is not."""
     q_lens = np.array([512], dtype=np.int64)
     kv = np.array([4806], dtype=np.int32)
     q_indptr = np.array([0, 512], dtype=np.int32)
@@ -157,7 +157,7 @@ def test_prefill_plan_splits_small_steps(num_cus):
         assert info.num_merge == 0 and real == 64
     else:
         assert info.num_merge == 64 and info.kv_chunk % 64 == 0 and info.kv_chunk >= 256
-        assert cus <= real <= 2 * cus + 64
+        assert 0.75 * cus <= real <= cus + 64
     big = np.full(16, 512, dtype=np.int64)
     qi = np.concatenate([[0], np.cumsum(big)]).astype(np.int32)
     kvb = np.full(16, 2048, dtype=np.int32)
