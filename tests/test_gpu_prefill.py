@@ -97,6 +97,42 @@ def test_prefill_split_kv_matches_oracle(device, ps):
     assert max_abs(out_s, want) <= ATOL
 
 
+@pytest.mark.parametrize("cus", [1, 1024])
+def test_prefill_graph_replays_and_repeats(device, cus):
+    """Prefill (whole items with one CU's plan; split KV ranges and the merge
+    with 1024 CUs' plan) captured in a HIP graph gives the eager result bit
+    for bit on every replay, with eager launches and synchronisation between
+    replays; repeated eager launches are bit-identical too."""
+    rng = np.random.default_rng(70)
+    q_lens, prefixes = [1, 77, 256, 300, 512], [700, 0, 1500, 33, 2048]
+    kv, indptr, indices, q_indptr = make_rows(rng, q_lens, prefixes, 16, 600)
+    pool = random_pool(600, 1, 4, 16, 128, device, 71)
+    q = random_tensor((int(q_indptr[-1]), 8, 128), device, 72)
+    table = table_from_csr(indptr, indices, kv, device)
+    qi = torch.from_numpy(q_indptr).to(device)
+    plan = PrefillPlan(q_indptr, kv, 8, 4, device, num_cus=cus)
+    assert (plan.info.num_merge > 0) == (cus == 1024)
+    ws = torch.empty(max(plan.workspace_bytes(), 1), dtype=torch.uint8, device=device)
+    out = torch.empty_like(q)
+    eager = paged_prefill(pool, 0, table, qi, q, plan, workspace=ws).clone()
+    for _ in range(3):
+        again = paged_prefill(pool, 0, table, qi, q, plan, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        paged_prefill(pool, 0, table, qi, q, plan, out=out, workspace=ws)
+    for r in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"
+        paged_prefill(pool, 0, table, qi, q, plan, workspace=ws)   # eager launch between replays
+        torch.cuda.synchronize()
+    want = oracle_prefill(pool, 0, q, q_indptr, indptr, indices, kv)
+    assert max_abs(eager, want) <= ATOL
+
+
 @pytest.mark.parametrize("ps", [4, 256])
 def test_prefill_long_rows_beyond_staged_page_ids(device, ps):
     """A row with more pages than a workgroup stages in LDS (2048) takes the
