@@ -283,6 +283,34 @@ int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
                            void* workspace_dev, int64_t workspace_bytes,
                            kunserve_stream_t stream);
 
+/* ------------------------------------------- fused page-id space (A6) */
+
+/* When N instances fuse into an N-stage pipeline (KunServe's balloon), each
+ * instance runs G = num_layers / N layers and its block manager numbers
+ * pages in the fused space (kunserve/block_manager.py:231-269):
+ *   - layer group i (layers [i*G, (i+1)*G)) of base page b is fused page
+ *     i * P + b, P = base pages before fusion (convert_to_pipeline_format,
+ *     :250-253; a stale request of rank r keeps r * P + b, :755-760);
+ *   - extend pages (the dropped weight memory, pages P.. of the pool) are
+ *     fused ids from P * N on (add_ex_fusion_blocks, :262-269), each of G
+ *     layers: extend page P + q holds fused pages P*N + q*N + i, i < N;
+ *   - pforward then receives max_num_pages = P*N + E
+ *     (kunserve/flash_backend.py:2433-2440).
+ * kunserve_fused_pool describes the same memory as a pool of
+ * num_pages * N pages of G layers, and kunserve_fused_page_ids turns fused
+ * ids into its page indices. Every other entry point then works unchanged
+ * on the fused pool, with stage-local layer indices. Nothing is copied:
+ * fused page r * P + b of stage r reads the bytes page b held before the
+ * fusion. Requires page_stride == num_layers * layer_stride. Host only. */
+int kunserve_fused_pool(const kunserve_kv_pool* pool, int64_t base_pages,
+                        int32_t fusion_size, kunserve_kv_pool* fused);
+
+/* Fused ids [0, num_fused_pages) -> page indices of the fused pool
+ * (num_fused_pages = P*N + E). KUNSERVE_ERANGE on an id outside. Host only. */
+int kunserve_fused_page_ids(const int32_t* fused_ids_host, int64_t n,
+                            int64_t base_pages, int32_t fusion_size,
+                            int64_t num_fused_pages, int32_t* pages_host);
+
 /* ------------------------------------ parameter memory remap (pmm_drop) */
 
 /* KV pools whose tail can be extended by the memory of dropped weight

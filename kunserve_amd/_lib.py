@@ -93,6 +93,9 @@ SIGNATURES = {
                                        POINTER(Tensor3), POINTER(Tensor3), c_int32, c_float,
                                        c_void_p, POINTER(PrefillPlanInfo), c_void_p, c_int64,
                                        c_void_p]),
+    "kunserve_fused_pool": (c_int, [POINTER(KVPool), c_int64, c_int32, POINTER(KVPool)]),
+    "kunserve_fused_page_ids": (c_int, [c_void_p, c_int64, c_int64, c_int32, c_int64,
+                                        c_void_p]),
     "kunserve_pmm_create": (c_int, [c_int32, c_int64, c_int64, c_int64, POINTER(c_void_p)]),
     "kunserve_pmm_add_segment": (c_int, [c_void_p, c_int64, POINTER(c_int32),
                                          POINTER(c_void_p)]),

@@ -51,3 +51,65 @@ int check_pool(const kunserve_kv_pool* p, bool need_vec_align) {
 extern "C" int32_t kunserve_version(void) { return 100; }
 
 extern "C" const char* kunserve_last_error(void) { return kunserve::g_last_error.c_str(); }
+
+// ------------------------------------------------ fused page-id space
+// A fusion group of N instances splits every base page of L layers into N
+// pages of G = L / N layers (kunserve/block_manager.py:231-269). For a pool
+// whose layers are contiguous within a page (page_stride == L *
+// layer_stride, the [pages, layers, heads, slots, dim] layout), layer group
+// i of page p is exactly page p * N + i of the same memory seen as
+// [num_pages * N, G, heads, slots, dim]; the fused ids are a renumbering of
+// those pages, so no kernel needs to know about fusion.
+
+extern "C" int kunserve_fused_pool(const kunserve_kv_pool* pool, int64_t base_pages,
+                                   int32_t fusion_size, kunserve_kv_pool* fused) {
+  using namespace kunserve;
+  clear_error();
+  int rc = check_pool(pool, false);
+  if (rc) return rc;
+  KSV_CHECK_ARG(fused != nullptr, "null output pool");
+  KSV_CHECK_ARG(fusion_size >= 1 && pool->num_layers % fusion_size == 0,
+                "%d layers do not split into %d equal stages", pool->num_layers, fusion_size);
+  KSV_CHECK_ARG(base_pages >= 1 && base_pages <= pool->num_pages,
+                "base_pages %lld outside [1, %lld]", (long long)base_pages,
+                (long long)pool->num_pages);
+  if (pool->page_stride != int64_t(pool->num_layers) * pool->layer_stride) {
+    set_error("fused pages need the layers of a page to be contiguous (page_stride %lld != "
+              "%d layers x layer_stride %lld)", (long long)pool->page_stride, pool->num_layers,
+              (long long)pool->layer_stride);
+    return KUNSERVE_EUNSUPPORTED;
+  }
+  const int64_t pages = pool->num_pages * fusion_size;
+  KSV_CHECK_ARG(pages < (int64_t(1) << 31), "%lld fused pages exceed 2^31", (long long)pages);
+  *fused = *pool;
+  fused->num_pages = pages;
+  fused->num_layers = pool->num_layers / fusion_size;
+  fused->page_stride = int64_t(fused->num_layers) * pool->layer_stride;
+  return KUNSERVE_OK;
+}
+
+extern "C" int kunserve_fused_page_ids(const int32_t* fused_ids_host, int64_t n,
+                                       int64_t base_pages, int32_t fusion_size,
+                                       int64_t num_fused_pages, int32_t* pages_host) {
+  using namespace kunserve;
+  clear_error();
+  KSV_CHECK_ARG(n >= 0 && (n == 0 || (fused_ids_host && pages_host)), "null id array");
+  KSV_CHECK_ARG(fusion_size >= 1 && base_pages >= 1, "bad fusion geometry");
+  const int64_t base_ids = base_pages * fusion_size;
+  KSV_CHECK_ARG(num_fused_pages >= base_ids && num_fused_pages < (int64_t(1) << 31),
+                "num_fused_pages %lld below the %lld fused base pages",
+                (long long)num_fused_pages, (long long)base_ids);
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t f = fused_ids_host[i];
+    if (f < 0 || f >= num_fused_pages) {
+      set_error("fused page id %lld outside [0, %lld)", (long long)f, (long long)num_fused_pages);
+      return KUNSERVE_ERANGE;
+    }
+    // Base ids i * P + b -> page b * N + i; extend ids (>= P * N) map to
+    // themselves: extend page P + q of the unfused pool is fused pages
+    // (P + q) * N + i = P * N + (q * N + i).
+    pages_host[i] = f < base_ids ? int32_t((f % base_pages) * fusion_size + f / base_pages)
+                                 : int32_t(f);
+  }
+  return KUNSERVE_OK;
+}

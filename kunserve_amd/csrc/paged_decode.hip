@@ -301,6 +301,7 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   static_assert(G <= 16, "one 16-column MFMA tile of query heads");
 
   __shared__ int s_pages[kMaxPartPages];
+  __shared__ int s_bad[kWaves];
   __shared__ __attribute__((aligned(16))) T s_kv[kWaves * BLK];   // 32 KiB: K, then V
   __shared__ float s_m[kWaves][G];
   __shared__ float s_l[kWaves][G];
@@ -324,10 +325,17 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   const int pb = tb >> a.page_shift;
   const int np = te > tb ? ((te - 1) >> a.page_shift) + 1 - pb : 0;
   const int32_t* seq_pages = a.indices + a.indptr[seq];
+  bool bad_id = false;
   for (int i = tid; i < np; i += kThreads) {
     const int p = seq_pages[pb + i];
-    s_pages[i] = (p >= 0 && p < a.num_pages) ? p : -1;
+    const bool ok = p >= 0 && p < a.num_pages;
+    s_pages[i] = ok ? p : -1;
+    bad_id |= !ok;
   }
+  // Whether any staged id is outside the pool (one vote per wave, read after
+  // the barrier below): only then do the scores need a per-page mask.
+  const bool wave_bad = __any(bad_id);
+  if (lane == 0) s_bad[wave] = wave_bad;
 
   // Q^T as the B operand: dim step s covers dims 32s + 8tg .. +8 of head j.
   V8 qb[4];
@@ -342,6 +350,10 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   float m = kNegBig;   // running max of head j, scaled log2 units (same in all tg)
   float lsum = 0.f;    // this lane's share of head j's sum
   __syncthreads();
+  int bad_votes = 0;
+#pragma unroll
+  for (int wv = 0; wv < kWaves; ++wv) bad_votes |= s_bad[wv];
+  const bool any_bad = __builtin_amdgcn_readfirstlane(bad_votes) != 0;   // the same in every lane
 
   const f16* kb = a.k + int64_t(hkv) * a.head_stride + lcol * 8;
   const f16* vb = a.v + int64_t(hkv) * a.head_stride + lcol * 8;
@@ -392,15 +404,24 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   // Softmax of the scores and O^T += V^T . P^T with the V rows in the block.
   auto accumulate = [&](f32x4 (&sc)[2], int c) {
     // Mask tokens past the partition; lane holds tokens 16 sub + 4 tg + v.
+    // Tokens of an out-of-range page id (their K/V rows read as zeros) are
+    // masked too, so they drop out of the softmax as in the VALU kernel; the
+    // 4 tokens of a lane share one page (page_size >= 4).
     const int t0 = tb + c * STEP;
     float mx = -INFINITY;
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+    for (int sub = 0; sub < 2; ++sub) {
+      bool bad_page = false;
+      if (any_bad) {
+        const int t = t0 + 16 * sub + 4 * tg;
+        bad_page = t < te && s_pages[min((t >> a.page_shift) - pb, kMaxPartPages - 1)] < 0;
+      }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        if (t0 + 16 * sub + 4 * tg + v >= te) sc[sub][v] = -INFINITY;
+        if (bad_page || t0 + 16 * sub + 4 * tg + v >= te) sc[sub][v] = -INFINITY;
         mx = fmaxf(mx, sc[sub][v]);
       }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
     if (__any(mx > m + 8.f)) {
@@ -717,6 +738,8 @@ extern "C" int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer
   KSV_CHECK_ARG(table && q && out && info, "null argument");
   KSV_CHECK_ARG(layer >= 0 && layer < pool->num_layers, "layer %d outside [0, %d)", layer,
                 pool->num_layers);
+  KSV_CHECK_ARG(std::isfinite(sm_scale) && sm_scale > 0.f,
+                "sm_scale %g must be finite and positive", double(sm_scale));
   KSV_CHECK_ARG(num_qo_heads > 0 && num_qo_heads % pool->num_kv_heads == 0,
                 "num_qo_heads %d not a multiple of num_kv_heads %d", num_qo_heads,
                 pool->num_kv_heads);

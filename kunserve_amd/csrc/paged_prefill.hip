@@ -26,6 +26,7 @@
 //    range over several workgroups; those write fp32 partials (O, running
 //    max, sum) and a merge kernel combines them in split order.
 #include <algorithm>
+#include <cmath>
 #include <vector>
 
 #include "common.hpp"
@@ -111,6 +112,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   typedef typename Vec<T>::v8 V8;
   typedef typename Vec<T>::v4 V4;
   __shared__ int s_pg[STAGED ? kMaxStagedPages : 1];
+  __shared__ int s_bad[kWaves];
   __shared__ __attribute__((aligned(16))) T sK[2 * kKHalves];
   __shared__ __attribute__((aligned(16))) T sV[2 * kVHalves];
 
@@ -146,14 +148,33 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   const int kv_end = min(prefix + min(q0 + kTileQ, q_len), kv_hi);   // exclusive
   const int ntiles = (kv_end + kTileKV - 1) / kTileKV;   // tiles [kv_lo / kTileKV, ntiles)
   const int pg_lo = kv_lo >> a.page_shift;   // first staged page
-  if constexpr (STAGED) {
+  // Stage (or, for rows with too many pages, only scan) the page ids of
+  // [kv_lo, kv_end). Whether any of them is outside the pool is voted per
+  // wave: only then do the scores need a per-page mask, which drops the
+  // tokens of such pages from the softmax.
+  bool any_bad = false;
+  {
     const int npg = kv_end > kv_lo ? ((kv_end - 1) >> a.page_shift) + 1 - pg_lo : 0;
+    bool bad_id = false;
     for (int i = threadIdx.x; i < npg; i += kThreads) {
       const int p = pages[pg_lo + i];
-      s_pg[i] = (p >= 0 && p < a.num_pages) ? p : -1;
+      const bool ok = p >= 0 && p < a.num_pages;
+      if constexpr (STAGED) s_pg[i] = ok ? p : -1;
+      bad_id |= !ok;
     }
+    const bool wave_bad = __any(bad_id);
+    if ((threadIdx.x & 63) == 0) s_bad[threadIdx.x >> 6] = wave_bad;
     __syncthreads();
+    int bad = 0;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) bad |= s_bad[wv];
+    any_bad = __builtin_amdgcn_readfirstlane(bad) != 0;   // the same in every lane
   }
+  // Whether kv token `tok` (< kv_end) lies on an out-of-range page.
+  auto bad_page = [&](int tok) {
+    const int p = STAGED ? s_pg[(tok >> a.page_shift) - pg_lo] : pages[tok >> a.page_shift];
+    return uint32_t(p) >= uint32_t(a.num_pages);
+  };
 
   // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
   V8 qf[8];
@@ -241,14 +262,21 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     }
     // Lane holds tokens n0 + 32mt + 8(v/4) + 4h + v%4 of query row r.
     float mx = -INFINITY;
-    if (n0 + kTileKV - 1 > wave_first_pos || n0 + kTileKV > kvl) {
+    if (n0 + kTileKV - 1 > wave_first_pos || n0 + kTileKV > kvl || any_bad) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int tok = n0 + 32 * mt + 8 * (v >> 2) + 4 * h + (v & 3);
-          if (tok > qpos || tok >= kvl) st[mt][v] = -INFINITY;
-          mx = fmaxf(mx, st[mt][v]);
+        for (int v4 = 0; v4 < 4; ++v4) {
+          // The 4 tokens of a group share one page (page_size >= 4).
+          const int tok0 = n0 + 32 * mt + 8 * v4 + 4 * h;
+          const bool skip = any_bad && tok0 < kv_end && bad_page(tok0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int v = 4 * v4 + e;
+            const int tok = tok0 + e;
+            if (skip || tok > qpos || tok >= kvl) st[mt][v] = -INFINITY;
+            mx = fmaxf(mx, st[mt][v]);
+          }
         }
     } else {
 #pragma unroll
@@ -891,6 +919,8 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   KSV_CHECK_ARG(table && q && out && info, "null argument");
   KSV_CHECK_ARG(layer >= 0 && layer < pool->num_layers, "layer %d outside [0, %d)", layer,
                 pool->num_layers);
+  KSV_CHECK_ARG(std::isfinite(sm_scale) && sm_scale > 0.f,
+                "sm_scale %g must be finite and positive", double(sm_scale));
   if (pool->head_dim != kD) {
     set_error("prefill kernel is compiled for head_dim %d, got %d", kD, pool->head_dim);
     return KUNSERVE_EUNSUPPORTED;

@@ -12,6 +12,17 @@ LlamaOp owns kv_data (kunserve/models.py:53). The dense parts of pforward
 (QKV / O / MLP GEMMs, RoPE, sampling) are outside this library: pforward
 here takes the step's host arguments and returns an AttentionStep whose
 run(layer, q, k, v) is the per-layer attention stage.
+
+Page ids follow the reference's block manager in both of its states:
+  * unfused: ids [0, P) name pages of all layers (P = max_num_pages);
+  * fused (a balloon group of N instances, kunserve/block_manager.py:231-269):
+    a pforward over one pipeline stage (local layers [r*G, (r+1)*G),
+    G = layers / N, kunserve/flash_backend.py:2442-2443) takes fused ids:
+    i*P + b is layer group i of base page b, and ids from P*N on are the
+    extend pages pmm_drop made, G layers each. The stage's layers live in
+    those G-layer pages, so a stale request that keeps id r*P + b
+    (kunserve/block_manager.py:755-760) reads the bytes page b held, with no
+    copy (KVPool.fused_view).
 """
 from __future__ import annotations
 
@@ -20,7 +31,8 @@ from typing import Dict, List, Optional, Sequence
 import numpy as np
 import torch
 
-from .paged_kv import AttentionStep, KVPool, copy_blocks, kv_pack, kv_scatter
+from .paged_kv import (AttentionStep, KVPool, copy_blocks, fused_page_ids, kv_pack,
+                       kv_scatter)
 from .pmm import PmmPool
 
 
@@ -41,9 +53,16 @@ class LlamaOp:
                  page_size: int, head_size: int, inter_size: int, vocab_size: int,
                  max_batch_size: int, max_batch_tokens: int, max_position_embeddings: int,
                  tensor_parallel_size: int, device: Optional[torch.device] = None,
-                 dtype: torch.dtype = torch.float16, max_extend_pages: int = 0):
+                 dtype: torch.dtype = torch.float16, max_extend_pages: int = 0,
+                 use_tensor_cores: bool = False):
+        """use_tensor_cores: the engine's --use-tensor-cores
+        (kunserve/kunserve_config.py:54-55), under which every row arrives
+        flagged as prefill (see kv_lens_for_step)."""
         if qo_head % kv_head:
             raise ValueError(f"qo_head {qo_head} is not a multiple of kv_head {kv_head}")
+        self.use_tensor_cores = use_tensor_cores
+        # Instances in the balloon group this op last joined (pmm_drop).
+        self.fusion_size = 1
         self.max_num_pages = max_num_pages
         self.layers = layers
         self.qo_head = qo_head
@@ -80,32 +99,66 @@ class LlamaOp:
                  input_tokens_batched: List[List[int]], first_token_indexes: List[int],
                  is_prefill_requests: List[int], pages_of_reqs: List[List[int]],
                  num_restore_requests: int = 0, pages_of_pp: Optional[List[List[int]]] = None,
-                 pages_of_dp: Optional[List[List[int]]] = None, receiver_rank: int = 0
-                 ) -> AttentionStep:
+                 pages_of_dp: Optional[List[List[int]]] = None, receiver_rank: int = 0,
+                 is_context_stage: Optional[List[int]] = None) -> AttentionStep:
         """Prepares the attention stage of one step (kunserve/worker.py:270-312).
 
-        Argument meanings follow kunserve/flash_backend.py:2448-2469. The
-        live-restore arguments (num_restore_requests, pages_of_pp,
-        pages_of_dp, receiver_rank) are accepted for signature parity; the
-        reference caller passes num_restore_requests = 0
-        (kunserve/flash_backend.py:2465).
+        Argument meanings follow kunserve/flash_backend.py:2448-2469. A layer
+        range that is one pipeline stage of the model (fusion execution,
+        kunserve/flash_backend.py:2442-2443) takes fused page ids below
+        max_num_pages = P*N + E (kunserve/flash_backend.py:2435-2440); the
+        whole model takes unfused ids. The live-restore arguments
+        (num_restore_requests, pages_of_pp, pages_of_dp, receiver_rank) are
+        accepted for signature parity; the reference caller passes
+        num_restore_requests = 0 (kunserve/flash_backend.py:2465).
+        is_context_stage (not in the reference signature) gives the rows'
+        real stages when use_tensor_cores hides them (kv_lens_for_step).
         """
         if len(input_tokens_batched) != num_requests or len(pages_of_reqs) != num_requests:
             raise ValueError("num_requests does not match the per-row argument lists")
         q_lens = [len(t) for t in input_tokens_batched]
         if sum(q_lens) != num_tokens:
             raise ValueError(f"num_tokens {num_tokens} != {sum(q_lens)} input tokens")
-        if not 0 <= local_layer_start <= local_layer_end <= self.layers:
+        if not 0 <= local_layer_start < local_layer_end <= self.layers:
             raise ValueError("local layer range outside the model")
-        if max_num_pages > self.max_num_pages:
-            raise ValueError(f"max_num_pages {max_num_pages} exceeds the pool "
-                             f"({self.max_num_pages})")
         if num_restore_requests:
             raise NotImplementedError("live KV restore inside pforward is not part of this path")
-        step = AttentionStep(self.pool, self.qo_head, q_lens, first_token_indexes,
-                             is_prefill_requests, pages_of_reqs)
+        stage_layers = local_layer_end - local_layer_start
+        if stage_layers == self.layers:
+            pool, id_map, num_ids, offset = self.pool, None, self.max_num_pages, 0
+        else:
+            if self.layers % stage_layers or local_layer_start % stage_layers:
+                raise ValueError(f"layers [{local_layer_start}, {local_layer_end}) are not one "
+                                 f"of {self.layers} // {stage_layers} equal pipeline stages")
+            n = self.layers // stage_layers
+            pool = self.fused_pool(n)
+            num_ids = pool.num_pages
+            base = self.num_base_pages
+
+            def id_map(ids, base=base, n=n, num_ids=num_ids):
+                return fused_page_ids(ids, base, n, num_ids)
+            offset = local_layer_start
+        if max_num_pages > num_ids:
+            raise ValueError(f"max_num_pages {max_num_pages} exceeds the pool "
+                             f"({num_ids} pages in this id space)")
+        step = AttentionStep(pool, self.qo_head, q_lens, first_token_indexes,
+                             is_prefill_requests, pages_of_reqs,
+                             use_tensor_cores=self.use_tensor_cores,
+                             is_context_stage=is_context_stage, layer_offset=offset,
+                             id_map=id_map, num_ids=min(max_num_pages, num_ids))
         step.layer_range = (local_layer_start, local_layer_end)
         return step
+
+    def fused_pool(self, fusion_size: int) -> KVPool:
+        """The pool in the fused page-id space of a group of fusion_size
+        instances (see the module docstring); fusion_size 1 is the pool."""
+        if fusion_size == 1:
+            return self.pool
+        return self.pool.fused_view(self.num_base_pages, fusion_size)
+
+    def num_fused_pages(self, fusion_size: int) -> int:
+        """P * N + E: the fused ids the block manager may hand out."""
+        return self.max_num_pages * fusion_size
 
     # ------------------------------------------------- parameter memory
 
@@ -124,15 +177,21 @@ class LlamaOp:
         return self.pmm.segment(self._weight_segments[layer])
 
     def pmm_drop(self, rank_in_group: int, num_group_instances: int) -> int:
-        """Drops the weights of every layer outside this instance's stage and
+        """Joins a balloon group of num_group_instances instances as stage
+        rank_in_group: drops the weights of every layer outside the stage and
         returns the number of KV blocks they became (kunserve/worker.py:454-458).
-        The new blocks are [num_base, num_base + returned) in order of the
-        dropped layers (kunserve/block_manager.py:262-269); K blocks take the
-        first half of each layer's memory and V blocks the second. Waits for
-        the device. Views of the dropped weights must not be used afterwards."""
-        if self.pmm is None:
-            raise RuntimeError("LlamaOp was built without max_extend_pages")
+        Blocks are counted as the fused stage uses them, G = layers /
+        num_group_instances layers each, and are the fused extend ids
+        [P*N, P*N + returned) (add_ex_fusion_blocks,
+        kunserve/block_manager.py:262-269), in order of the dropped layers.
+        K takes the first half of each layer's memory and V the second. Waits
+        for the device. Views of the dropped weights must not be used
+        afterwards. Without max_extend_pages nothing can be dropped and 0 is
+        returned."""
         keep = kept_layers(self.layers, rank_in_group, num_group_instances)
+        self.fusion_size = num_group_instances
+        if self.pmm is None:
+            return 0
         dropped = set(self.dropped_layers())
         added = 0
         for layer in sorted(self._weight_segments):
@@ -140,7 +199,7 @@ class LlamaOp:
                 continue
             added += len(self.pmm.drop(self._weight_segments[layer]))
         self._sync_pool()
-        return added
+        return added * num_group_instances
 
     def pmm_restore(self) -> List[int]:
         """Maps every dropped layer's memory back to its weights and returns
@@ -172,16 +231,29 @@ class LlamaOp:
 
     def local_copy_blocks(self, max_num_pages: int, all_ex_blocks: Sequence[int],
                           all_base_blocks: Sequence[int]) -> None:
-        """Copies extend-region blocks into base-region blocks, all layers
-        (kunserve/worker.py:818-823; caller kunserve/flash_backend.py:1116-1123)."""
+        """Copies extend-region blocks into base-region blocks, all layers of
+        a block (kunserve/worker.py:818-823; caller
+        kunserve/flash_backend.py:1116-1123). In a balloon group (after
+        pmm_drop with N > 1) max_num_pages = P*N + E names the fused id space
+        (kunserve/flash_backend.py:2435-2440) and a block is a fused page of
+        layers / N layers; otherwise ids name whole pages."""
         if len(all_ex_blocks) != len(all_base_blocks):
             raise ValueError("ex and base block lists differ in length")
+        fused = self.fusion_size > 1 and max_num_pages > self.max_num_pages
+        limit = min(max_num_pages, self.num_fused_pages(self.fusion_size) if fused
+                    else self.max_num_pages)
         ids = np.asarray(list(all_ex_blocks) + list(all_base_blocks), dtype=np.int64)
-        if ids.size and (ids.min() < 0 or ids.max() >= min(max_num_pages, self.max_num_pages)):
-            raise IndexError(f"block id outside [0, {min(max_num_pages, self.max_num_pages)})")
+        if ids.size and (ids.min() < 0 or ids.max() >= limit):
+            raise IndexError(f"block id outside [0, {limit})")
         if len(set(all_ex_blocks) & set(all_base_blocks)):
             raise ValueError("source and destination blocks overlap")
-        copy_blocks(self.pool, all_ex_blocks, all_base_blocks)
+        if not fused:
+            copy_blocks(self.pool, all_ex_blocks, all_base_blocks)
+            return
+        pool = self.fused_pool(self.fusion_size)
+        n = self.fusion_size
+        copy_blocks(pool, fused_page_ids(all_ex_blocks, self.num_base_pages, n, pool.num_pages),
+                    fused_page_ids(all_base_blocks, self.num_base_pages, n, pool.num_pages))
 
     def kv_exchange_pack(self, page_ids: Sequence[int], layer_begin: int, layer_end: int,
                          scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -192,9 +264,23 @@ class LlamaOp:
 
     def kv_exchange_scatter(self, page_ids: Sequence[int], layer_begin: int, layer_end: int,
                             scratch: torch.Tensor) -> None:
-        """kv_exchange phase 3: writes received pages into fused page ids
-        (kunserve/block_manager.py:755-763)."""
-        kv_scatter(self.pool, layer_begin, layer_end, page_ids, scratch)
+        """kv_exchange phase 3: writes received pages into this instance's
+        fused page ids (kunserve/block_manager.py:755-763). Layers
+        [layer_begin, layer_end) are model layers of this instance's stage in
+        its balloon group (pmm_drop); they land in the fused pages' G-layer
+        slabs. Outside a group the ids are whole pages."""
+        n = self.fusion_size
+        if n == 1:
+            kv_scatter(self.pool, layer_begin, layer_end, page_ids, scratch)
+            return
+        g = self.layers // n
+        stage = layer_begin // g
+        if not (0 <= layer_begin < layer_end <= (stage + 1) * g):
+            raise ValueError(f"layers [{layer_begin}, {layer_end}) are not within one stage "
+                             f"of {g} layers")
+        pool = self.fused_pool(n)
+        ids = fused_page_ids(page_ids, self.num_base_pages, n, pool.num_pages)
+        kv_scatter(pool, layer_begin - stage * g, layer_end - stage * g, ids, scratch)
 
     def kv_exchange(self, pages_of_instances: List[List[int]], pp_rank: int, pp_size: int,
                     group_rank: int, group_size: int, num_base_blocks: int,

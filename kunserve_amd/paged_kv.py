@@ -18,7 +18,7 @@ from __future__ import annotations
 import ctypes
 import math
 from dataclasses import dataclass
-from typing import Optional, Sequence
+from typing import Callable, Optional, Sequence
 
 import numpy as np
 import torch
@@ -38,6 +38,29 @@ def _stream_ptr(device: torch.device) -> int:
 
 def _i32(x) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+
+
+def _upload(arr: np.ndarray, device: torch.device) -> torch.Tensor:
+    """A new device tensor holding `arr`, enqueued on the current stream with
+    no host wait: the bytes go through a pinned buffer of torch's caching
+    host allocator, which keeps that buffer from reuse until the copy ran."""
+    src = torch.from_numpy(np.ascontiguousarray(arr))
+    staged = torch.empty(src.shape, dtype=src.dtype, pin_memory=True)
+    staged.copy_(src)
+    return staged.to(device, non_blocking=True)
+
+
+def _upload_packed(arrays: Sequence[np.ndarray], device: torch.device) -> list:
+    """Uploads several int32 host arrays with one copy; returns a device
+    view per array (all views share one allocation)."""
+    sizes = [int(a.size) for a in arrays]
+    dev = _upload(np.concatenate([_i32(a).reshape(-1) for a in arrays]) if arrays
+                  else np.zeros(0, np.int32), device)
+    out, at = [], 0
+    for n in sizes:
+        out.append(dev[at:at + n])
+        at += n
+    return out
 
 
 _DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
@@ -96,39 +119,113 @@ class KVPool:
                                "use the owner's current pool")
         return ctypes.byref(self._desc)
 
+    def fused_view(self, base_pages: int, fusion_size: int) -> "KVPool":
+        """The pool as a fusion group of `fusion_size` instances addresses it
+        (kunserve/block_manager.py:231-269): each page of L layers becomes
+        fusion_size pages of L / fusion_size layers. Layer group i of base
+        page b is fused page i * base_pages + b, and page base_pages + q of
+        the extend region (pages past the base ones) holds fused extend pages
+        base_pages * fusion_size + q * fusion_size + i. Nothing is copied: the
+        view has num_pages * fusion_size pages of L / fusion_size layers over
+        the same memory (kunserve_fused_pool), and fused ids are turned into
+        its page indices by fused_page_ids."""
+        desc = _lib.KVPool()
+        _lib.call("kunserve_fused_pool", ctypes.byref(self._desc), base_pages, fusion_size,
+                  ctypes.byref(desc))
+        shape = (desc.num_pages, desc.num_layers, self.num_kv_heads, self.page_size,
+                 self.head_dim)
+        strides = (desc.page_stride, desc.layer_stride) + tuple(self.k.stride()[2:])
+        k = self.k.as_strided(shape, strides, self.k.storage_offset())
+        v = self.v.as_strided(shape, strides, self.v.storage_offset())
+        view = KVPool(k, v, owner=self._owner)
+        view._generation = self._generation
+        view.base_pages, view.fusion_size = base_pages, fusion_size
+        return view
+
+
+def fused_page_ids(ids, base_pages: int, fusion_size: int, num_fused_pages: int) -> np.ndarray:
+    """Fused page ids (kunserve/block_manager.py:250-253,262-269) -> pages of
+    KVPool.fused_view(base_pages, fusion_size) (kunserve_fused_page_ids)."""
+    arr = _i32(ids).reshape(-1)
+    out = np.empty_like(arr)
+    _lib.call("kunserve_fused_page_ids", arr.ctypes.data, arr.size, base_pages, fusion_size,
+              num_fused_pages, out.ctypes.data)
+    return out
+
 
 # ------------------------------------------------------------ step arguments
 
 
 def kv_lens_for_step(first_token_indexes: Sequence[int], q_lens: Sequence[int],
-                     is_prefill_requests: Sequence[int]) -> np.ndarray:
+                     is_prefill_requests: Sequence[int], use_tensor_cores: bool = False,
+                     is_context_stage: Optional[Sequence[int]] = None) -> np.ndarray:
     """KV length of each row after this step's tokens are appended.
 
     kunserve/request.py:447-462: a prefill row's first index is
     prefill_begin_index (tokens already cached), so kv_len = first + q_len;
     a decode row's first index is prompt_len + output_len, which already
     counts the token being decoded (the block allocation of
-    kunserve/request.py:414-423 uses the same count), so kv_len = first.
-    In both cases the new tokens occupy positions [kv_len - q_len, kv_len).
+    kunserve/request.py:414-423 and kunserve/block_manager.py:493-500 uses
+    the same count), so kv_len = first. In both cases the new tokens occupy
+    positions [kv_len - q_len, kv_len).
+
+    With use_tensor_cores every row arrives flagged as prefill
+    (kunserve/request.py:667-670, kunserve/flash_backend.py:2460-2462), so
+    the flag no longer tells a decode row from a one-token prefill chunk.
+    Rows with one input token and a first index > 0 are then taken as decode
+    rows (kv_len = first), which keeps every append inside the blocks the
+    block manager allocated; a one-token row at first index 0 can only be
+    the first chunk of a one-token prompt (kv_len = 1). A one-token prefill
+    chunk at first index > 0 (the last chunk of a prompt one token longer
+    than a chunk multiple) is the case these arguments cannot separate: the
+    caller passes the rows' real stages as is_context_stage
+    ([int(r.is_context_stage()) for r in requests]), which then decides for
+    every row instead of the flags.
     """
     first = np.asarray(first_token_indexes, dtype=np.int64)
     ql = np.asarray(q_lens, dtype=np.int64)
-    flag = np.asarray(is_prefill_requests, dtype=np.int64)
-    if not (first.shape == ql.shape == flag.shape):
-        raise ValueError("first_token_indexes, q_lens and is_prefill_requests differ in length")
-    kv = np.where(flag != 0, first + ql, first)
+    decode = decode_rows(first_token_indexes, q_lens, is_prefill_requests, use_tensor_cores,
+                         is_context_stage)
+    if np.any(decode & (ql != 1)):
+        bad = int(np.argmax(decode & (ql != 1)))
+        raise ValueError(f"row {bad}: a decode row takes exactly one input token, got {ql[bad]}")
+    kv = np.where(decode, first, first + ql)
     if np.any(kv < ql):
         bad = int(np.argmax(kv < ql))
         raise ValueError(f"row {bad}: kv_len {kv[bad]} shorter than its {ql[bad]} new tokens")
     return kv.astype(np.int32)
 
 
+def decode_rows(first_token_indexes: Sequence[int], q_lens: Sequence[int],
+                is_prefill_requests: Sequence[int], use_tensor_cores: bool = False,
+                is_context_stage: Optional[Sequence[int]] = None) -> np.ndarray:
+    """Boolean mask of the decode rows of a step, by the rule of
+    kv_lens_for_step."""
+    first = np.asarray(first_token_indexes, dtype=np.int64)
+    ql = np.asarray(q_lens, dtype=np.int64)
+    flag = np.asarray(is_prefill_requests, dtype=np.int64)
+    if not (first.shape == ql.shape == flag.shape):
+        raise ValueError("first_token_indexes, q_lens and is_prefill_requests differ in length")
+    if is_context_stage is not None:
+        stage = np.asarray(is_context_stage, dtype=np.int64)
+        if stage.shape != first.shape:
+            raise ValueError("is_context_stage differs in length from the other row arguments")
+        return stage == 0
+    if use_tensor_cores:
+        return (flag == 0) | ((ql == 1) & (first > 0))
+    return flag == 0
+
+
 def csr_from_lists(pages_of_reqs: Sequence[Sequence[int]], kv_len: np.ndarray,
-                   page_size: int, num_pages: int) -> tuple[np.ndarray, np.ndarray]:
+                   page_size: int, num_pages: int,
+                   id_map: Optional[Callable[[np.ndarray], np.ndarray]] = None
+                   ) -> tuple[np.ndarray, np.ndarray]:
     """Ragged page lists -> (indptr, indices) int32, validated.
 
     Each row must hold at least ceil(kv_len / page_size) pages
-    (kunserve/block_manager.py:493-500,786-795); only those are kept.
+    (kunserve/block_manager.py:493-500,786-795); only those are kept. Ids
+    must lie in [0, num_pages); id_map, if given, then turns them into the
+    page indices the kernels use (fused ids -> pages of a fused view).
     """
     n = len(pages_of_reqs)
     if len(kv_len) != n:
@@ -146,39 +243,55 @@ def csr_from_lists(pages_of_reqs: Sequence[Sequence[int]], kv_len: np.ndarray,
     if indices.size and (indices.min() < 0 or indices.max() >= num_pages):
         bad = int(indices[(indices < 0) | (indices >= num_pages)][0])
         raise IndexError(f"page id {bad} outside the pool [0, {num_pages})")
-    return indptr.astype(np.int32), indices.astype(np.int32)
+    indices = indices.astype(np.int32)
+    if id_map is not None:
+        indices = _i32(id_map(indices))
+    return indptr.astype(np.int32), indices
 
 
 class PageTable:
-    """Per-step CSR page table, on the device and mirrored on the host."""
+    """Per-step CSR page table, on the device and mirrored on the host.
+
+    The device copy is enqueued on the current stream through pinned memory
+    (no host wait). With upload=False nothing is copied until bind() is given
+    device views of host_arrays() (AttentionStep uploads all of a step's
+    arrays with one copy)."""
 
     def __init__(self, indptr: np.ndarray, indices: np.ndarray, kv_len: np.ndarray,
-                 device: torch.device):
+                 device: torch.device, upload: bool = True):
         self.indptr_host = _i32(indptr)
         self.indices_host = _i32(indices)
         self.kv_len_host = _i32(kv_len)
         self.num_seqs = len(self.kv_len_host)
+        self.device = device
         if len(self.indptr_host) != self.num_seqs + 1:
             raise ValueError("indptr must have num_seqs + 1 entries")
-        # One upload for the three arrays.
-        packed = np.concatenate([self.indptr_host, self.kv_len_host, self.indices_host])
-        dev = torch.from_numpy(packed).to(device, non_blocking=False)
-        n = self.num_seqs
-        self.indptr = dev[: n + 1]
-        self.kv_len = dev[n + 1: 2 * n + 1]
-        self.indices = dev[2 * n + 1:]
-        self._storage = dev
+        self._desc = None
+        if upload:
+            self.bind(_upload_packed(self.host_arrays(), device))
+
+    def host_arrays(self) -> list:
+        return [self.indptr_host, self.kv_len_host, self.indices_host]
+
+    def bind(self, dev: Sequence[torch.Tensor]) -> None:
+        self.indptr, self.kv_len, self.indices = dev
         self._desc = _lib.PageTable(self.indptr.data_ptr(), self.indices.data_ptr(),
-                                    self.kv_len.data_ptr(), n)
+                                    self.kv_len.data_ptr(), self.num_seqs)
 
     @classmethod
-    def from_lists(cls, pages_of_reqs: Sequence[Sequence[int]], kv_len, pool: KVPool
-                   ) -> "PageTable":
+    def from_lists(cls, pages_of_reqs: Sequence[Sequence[int]], kv_len, pool: KVPool,
+                   id_map: Optional[Callable[[np.ndarray], np.ndarray]] = None,
+                   num_ids: Optional[int] = None, upload: bool = True) -> "PageTable":
+        """num_ids: bound of the ids the lists may hold (default: the pool's
+        pages); id_map turns valid ids into pool pages."""
         kv = _i32(kv_len)
-        indptr, indices = csr_from_lists(pages_of_reqs, kv, pool.page_size, pool.num_pages)
-        return cls(indptr, indices, kv, pool.device)
+        indptr, indices = csr_from_lists(pages_of_reqs, kv, pool.page_size,
+                                         pool.num_pages if num_ids is None else num_ids, id_map)
+        return cls(indptr, indices, kv, pool.device, upload)
 
     def desc(self):
+        if self._desc is None:
+            raise RuntimeError("page table used before its device arrays were bound")
         return ctypes.byref(self._desc)
 
 
@@ -199,7 +312,8 @@ class DecodePlan:
     shared by every layer (kunserve_decode_plan)."""
 
     def __init__(self, kv_len_host: Sequence[int], num_qo_heads: int, num_kv_heads: int,
-                 device: torch.device, part_tokens: int = 0, num_cus: Optional[int] = None):
+                 device: torch.device, part_tokens: int = 0, num_cus: Optional[int] = None,
+                 upload: bool = True):
         kv = _i32(kv_len_host)
         n = len(kv)
         cap = _lib.lib().kunserve_decode_plan_bound(kv.ctypes.data if n else None, n)
@@ -210,9 +324,17 @@ class DecodePlan:
                   num_kv_heads, cus, part_tokens, buf.ctypes.data, buf.size,
                   ctypes.byref(self.info))
         self.plan_host = buf[: self.info.plan_ints].copy()
-        self.plan = torch.from_numpy(self.plan_host).to(device) if self.info.plan_ints else None
+        self.plan = None
+        if upload:
+            self.bind(_upload_packed(self.host_arrays(), device))
         self.num_qo_heads = num_qo_heads
         self.num_kv_heads = num_kv_heads
+
+    def host_arrays(self) -> list:
+        return [self.plan_host]
+
+    def bind(self, dev: Sequence[torch.Tensor]) -> None:
+        self.plan = dev[0] if self.info.plan_ints else None
 
     def workspace_bytes(self, head_dim: int) -> int:
         return int(_lib.lib().kunserve_decode_workspace_bytes(
@@ -226,7 +348,7 @@ class PrefillPlan:
 
     def __init__(self, q_indptr_host: Sequence[int], kv_len_host: Sequence[int],
                  num_qo_heads: int, num_kv_heads: int, device: torch.device,
-                 num_cus: Optional[int] = None):
+                 num_cus: Optional[int] = None, upload: bool = True):
         qi = _i32(q_indptr_host)
         kv = _i32(kv_len_host)
         n = len(kv)
@@ -240,7 +362,15 @@ class PrefillPlan:
                   num_qo_heads, num_kv_heads, cus, buf.ctypes.data, buf.size,
                   ctypes.byref(self.info))
         self.plan_host = buf[: self.info.plan_ints].copy()
-        self.plan = torch.from_numpy(self.plan_host).to(device) if self.info.plan_ints else None
+        self.plan = None
+        if upload:
+            self.bind(_upload_packed(self.host_arrays(), device))
+
+    def host_arrays(self) -> list:
+        return [self.plan_host]
+
+    def bind(self, dev: Sequence[torch.Tensor]) -> None:
+        self.plan = dev[0] if self.info.plan_ints else None
 
     def workspace_bytes(self) -> int:
         return int(_lib.lib().kunserve_prefill_workspace_bytes(ctypes.byref(self.info)))
@@ -270,7 +400,7 @@ def _ids_on_device(ids, pool: KVPool) -> torch.Tensor:
     arr = np.asarray(ids, dtype=np.int64).reshape(-1)
     if arr.size and (arr.min() < 0 or arr.max() >= pool.num_pages):
         raise IndexError(f"block id outside the pool [0, {pool.num_pages})")
-    return torch.from_numpy(arr.astype(np.int32)).to(pool.device)
+    return _upload(arr.astype(np.int32), pool.device)
 
 
 def kv_pack(pool: KVPool, layer_begin: int, layer_end: int, page_ids,
@@ -349,7 +479,7 @@ def rope_inv_freq(head_dim: int, theta: float = 10000.0,
     inv = 1.0 / (np.float32(theta) ** (np.arange(0, head_dim, 2, dtype=np.float32)
                                        / np.float32(head_dim)))
     t = torch.from_numpy(inv.astype(np.float32))
-    return t.to(device) if device is not None else t
+    return _upload(t.numpy(), device) if device is not None else t
 
 
 def rope_append_kv(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Tensor,
@@ -424,7 +554,7 @@ def paged_prefill(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Te
 @dataclass
 class _Subset:
     rows: np.ndarray            # row indices into the batch
-    tokens: Optional[torch.Tensor]  # token indices into q (None: all tokens, in order)
+    tokens: Optional[torch.Tensor]  # int32 token indices into q (None: all tokens, in order)
     table: PageTable
     q_indptr: Optional[torch.Tensor]
     plan: object
@@ -435,58 +565,114 @@ class AttentionStep:
     the step's host arguments and run for every layer.
 
     Per layer: append the new K/V of every row, then decode attention for
-    decode rows (q_len == 1, flag 0) and causal chunked-prefill attention for
-    prefill rows (flag 1; with use_tensor_cores every row is flagged,
-    kunserve/request.py:667-670).
+    decode rows and causal chunked-prefill attention for the others. Which
+    rows decode follows kv_lens_for_step (flag 0; with use_tensor_cores,
+    where every row is flagged, kunserve/request.py:667-670, one-token rows
+    past position 0).
+
+    pool may be a fused view (KVPool.fused_view); id_map then turns the
+    page lists' fused ids into its pages, and num_ids bounds those ids.
+    run(layer, ...) addresses pool layer layer - layer_offset, so a fused
+    stage runs its global layer indices on its local layers.
+
+    All of the step's index arrays (tables, plans, row and token indices)
+    reach the device in one copy on the current stream, with no host wait.
     """
 
     def __init__(self, pool: KVPool, num_qo_heads: int, q_lens: Sequence[int],
                  first_token_indexes: Sequence[int], is_prefill_requests: Sequence[int],
                  pages_of_reqs: Sequence[Sequence[int]], sm_scale: Optional[float] = None,
-                 decode_part_tokens: int = 0):
+                 decode_part_tokens: int = 0, use_tensor_cores: bool = False,
+                 is_context_stage: Optional[Sequence[int]] = None, layer_offset: int = 0,
+                 id_map: Optional[Callable[[np.ndarray], np.ndarray]] = None,
+                 num_ids: Optional[int] = None):
         self.pool = pool
         self.num_qo_heads = num_qo_heads
+        self.layer_offset = layer_offset
         dev = pool.device
         q_lens = np.asarray(q_lens, dtype=np.int64)
-        flags = np.asarray(is_prefill_requests, dtype=np.int64)
+        if len(pages_of_reqs) != len(q_lens):
+            raise ValueError(f"{len(q_lens)} rows but {len(pages_of_reqs)} page lists")
         if np.any(q_lens < 1):
             raise ValueError("every row needs at least one input token")
-        if np.any((flags == 0) & (q_lens != 1)):
-            raise ValueError("decode rows (flag 0) must have exactly one input token")
-        self.kv_len = kv_lens_for_step(first_token_indexes, q_lens, flags)
+        self.kv_len = kv_lens_for_step(first_token_indexes, q_lens, is_prefill_requests,
+                                       use_tensor_cores, is_context_stage)
+        is_decode = decode_rows(first_token_indexes, q_lens, is_prefill_requests,
+                                use_tensor_cores, is_context_stage)
         self.q_indptr_host = np.zeros(len(q_lens) + 1, dtype=np.int32)
         np.cumsum(q_lens, out=self.q_indptr_host[1:])
         self.num_tokens = int(self.q_indptr_host[-1])
-        self.table = PageTable.from_lists(pages_of_reqs, self.kv_len, pool)
-        self.q_indptr = torch.from_numpy(self.q_indptr_host).to(dev)
+        n_rows = len(q_lens)
+        self.table = PageTable.from_lists(pages_of_reqs, self.kv_len, pool, id_map, num_ids,
+                                          upload=False)
         self.scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(pool.head_dim)
+        if not (math.isfinite(self.scale) and self.scale > 0):
+            raise ValueError(f"sm_scale {self.scale} must be finite and positive")
 
+        # Host side of every device array of the step; uploaded together below.
+        uploads = [[self.q_indptr_host], self.table]
         self.decode = self.prefill = None
-        all_rows = np.arange(len(q_lens))
-        dec_rows = all_rows[flags == 0]
-        pre_rows = all_rows[flags != 0]
+        all_rows = np.arange(n_rows)
+        dec_rows, pre_rows = all_rows[is_decode], all_rows[~is_decode]
+        # Row subsets take their rows from the step's CSR arrays (ids already
+        # checked and mapped), not from the lists again.
+        def sub_table(rows):
+            lo, hi = self.table.indptr_host[rows], self.table.indptr_host[rows + 1]
+            indptr = np.concatenate([[0], np.cumsum(hi - lo)]).astype(np.int32)
+            indices = (np.concatenate([self.table.indices_host[a:b] for a, b in zip(lo, hi)])
+                       if rows.size else np.zeros(0, np.int32))
+            return PageTable(indptr, indices, self.kv_len[rows], dev, upload=False)
+
         if dec_rows.size:
-            sub_pages = [pages_of_reqs[i] for i in dec_rows]
-            table = (self.table if dec_rows.size == len(q_lens)
-                     else PageTable.from_lists(sub_pages, self.kv_len[dec_rows], pool))
-            tokens = (None if dec_rows.size == len(q_lens)
-                      else torch.from_numpy(self.q_indptr_host[dec_rows].astype(np.int64)).to(dev))
+            whole = dec_rows.size == n_rows
+            table = self.table if whole else sub_table(dec_rows)
+            tokens = None if whole else self.q_indptr_host[dec_rows].astype(np.int32)
             plan = DecodePlan(self.kv_len[dec_rows], num_qo_heads, pool.num_kv_heads, dev,
-                              part_tokens=decode_part_tokens)
+                              part_tokens=decode_part_tokens, upload=False)
             self.decode = _Subset(dec_rows, tokens, table, None, plan)
+            uploads += ([] if whole else [table, [tokens]]) + [plan]
         if pre_rows.size:
-            if pre_rows.size == len(q_lens):
+            whole = pre_rows.size == n_rows
+            if whole:
                 table, tokens, qi = self.table, None, self.q_indptr_host
             else:
-                table = PageTable.from_lists([pages_of_reqs[i] for i in pre_rows],
-                                             self.kv_len[pre_rows], pool)
-                tok = np.concatenate([np.arange(self.q_indptr_host[i], self.q_indptr_host[i + 1])
-                                      for i in pre_rows])
-                tokens = torch.from_numpy(tok.astype(np.int64)).to(dev)
+                table = sub_table(pre_rows)
+                tokens = np.concatenate([np.arange(self.q_indptr_host[i],
+                                                   self.q_indptr_host[i + 1])
+                                         for i in pre_rows]).astype(np.int32)
                 qi = np.zeros(pre_rows.size + 1, dtype=np.int32)
                 np.cumsum(q_lens[pre_rows], out=qi[1:])
-            plan = PrefillPlan(qi, self.kv_len[pre_rows], num_qo_heads, pool.num_kv_heads, dev)
-            self.prefill = _Subset(pre_rows, tokens, table, torch.from_numpy(qi).to(dev), plan)
+            plan = PrefillPlan(qi, self.kv_len[pre_rows], num_qo_heads, pool.num_kv_heads, dev,
+                               upload=False)
+            self.prefill = _Subset(pre_rows, tokens, table, None, plan)
+            uploads += ([] if whole else [table, [tokens], [qi]]) + [plan]
+
+        # One copy for all of them.
+        flat, owners = [], []
+        for u in uploads:
+            arrays = u if isinstance(u, list) else u.host_arrays()
+            owners.append((u, len(arrays)))
+            flat += arrays
+        views = _upload_packed(flat, dev)
+        at = 0
+        bound = []
+        for u, n in owners:
+            part = views[at:at + n]
+            at += n
+            if isinstance(u, list):
+                bound.append(part)
+            else:
+                u.bind(part)
+        self.q_indptr = bound[0][0]
+        rest = iter(bound[1:])
+        if self.decode is not None and self.decode.tokens is not None:
+            self.decode.tokens = next(rest)[0]
+        if self.prefill is not None:
+            if self.prefill.tokens is not None:
+                self.prefill.tokens = next(rest)[0]
+                self.prefill.q_indptr = next(rest)[0]
+            else:
+                self.prefill.q_indptr = self.q_indptr
         # Scratch shared by every layer of the step (launches are serialised on one stream).
         ws = max(self.decode.plan.workspace_bytes(pool.head_dim) if self.decode else 0,
                  self.prefill.plan.workspace_bytes() if self.prefill else 0)
@@ -502,30 +688,34 @@ class AttentionStep:
         are taken as already rotated."""
         if q.shape[0] != self.num_tokens or k.shape[0] != self.num_tokens:
             raise ValueError(f"expected {self.num_tokens} tokens, got q {q.shape[0]}, k {k.shape[0]}")
+        local = layer - self.layer_offset
+        if not 0 <= local < self.pool.num_layers:
+            raise ValueError(f"layer {layer} outside this step's layers "
+                             f"[{self.layer_offset}, {self.layer_offset + self.pool.num_layers})")
         if rope is not None:
             inv_freq, interleave = rope
-            rope_append_kv(self.pool, layer, self.table, self.q_indptr, q, k, v, inv_freq,
+            rope_append_kv(self.pool, local, self.table, self.q_indptr, q, k, v, inv_freq,
                            interleave)
         else:
-            append_kv(self.pool, layer, self.table, self.q_indptr, k, v)
+            append_kv(self.pool, local, self.table, self.q_indptr, k, v)
         if out is None:
             out = torch.empty_like(q)
         if self.decode is not None:
             d = self.decode
             if d.tokens is None:
-                paged_decode(self.pool, layer, d.table, q, d.plan, self.scale, out=out,
+                paged_decode(self.pool, local, d.table, q, d.plan, self.scale, out=out,
                              workspace=self.workspace)
             else:
-                out[d.tokens] = paged_decode(self.pool, layer, d.table,
-                                             q.index_select(0, d.tokens).contiguous(), d.plan,
+                out[d.tokens] = paged_decode(self.pool, local, d.table,
+                                             q.index_select(0, d.tokens), d.plan,
                                              self.scale, workspace=self.workspace)
         if self.prefill is not None:
             p = self.prefill
             if p.tokens is None:
-                paged_prefill(self.pool, layer, p.table, p.q_indptr, q, p.plan, self.scale,
+                paged_prefill(self.pool, local, p.table, p.q_indptr, q, p.plan, self.scale,
                               out=out, workspace=self.workspace)
             else:
-                out[p.tokens] = paged_prefill(self.pool, layer, p.table, p.q_indptr,
-                                              q.index_select(0, p.tokens).contiguous(), p.plan,
+                out[p.tokens] = paged_prefill(self.pool, local, p.table, p.q_indptr,
+                                              q.index_select(0, p.tokens), p.plan,
                                               self.scale, workspace=self.workspace)
         return out

@@ -23,7 +23,10 @@ reference's Python call sites, in plain numpy (float64 by default):
   kv_pack/kv_scatter  kv_exchange phases 1 and 3        kunserve/flash_backend.py:857-1022
   kv_lens_for_step    first_token_indexes rule          kunserve/request.py:414-462,654-670
   fused_page_ids,     fused / extend page-id space      kunserve/block_manager.py:250-253,
-  extend_page_ids                                       262-269, 755-760
+  extend_page_ids,                                      262-269, 755-760
+  kept_page_id,
+  fused_slab,         which (page, layer) of the pool a fused page uses (same lines;
+  fused_pool_copy     the extend layout is a convention, see fused_slab)
 
 Pinning (tests/test_oracle.py): attention is checked against
 torch.nn.functional.scaled_dot_product_attention on dense K/V written into
@@ -31,7 +34,10 @@ pages by an independent loop, and against closed forms (kv_len 1, q = 0,
 page permutation, GQA = repeated-KV MHA, prefill row = decode over its
 prefix); block movement is checked bit-exactly against element-wise loops on
 pools filled with unique values; kv_lens_for_step against a restated
-request lifecycle. No reference golden vectors exist in the reference tree.
+request lifecycle (also with every row flagged, the use_tensor_cores mode);
+the fused map by the invariants the block manager relies on (a kept id
+reads its page's bytes in place, fused ids partition the pool's slabs). No
+reference golden vectors exist in the reference tree.
 """
 from __future__ import annotations
 
@@ -217,13 +223,24 @@ def kv_scatter(k_pool: np.ndarray, v_pool: np.ndarray, layer_begin: int, layer_e
 
 
 def kv_lens_for_step(first_token_indexes: Sequence[int], q_lens: Sequence[int],
-                     is_prefill_requests: Sequence[int]) -> np.ndarray:
+                     is_prefill_requests: Sequence[int], use_tensor_cores: bool = False,
+                     is_context_stage: Sequence[int] | None = None) -> np.ndarray:
     """kv_len after append. Prefill rows: first = prefill_begin_index, so
     first + q_len; decode rows: first = prompt_len + output_len, which
-    already counts the token being decoded (kunserve/request.py:414-462)."""
+    already counts the token being decoded (kunserve/request.py:414-462).
+    With use_tensor_cores every row is flagged prefill
+    (kunserve/request.py:667-670); a one-token row past position 0 is then
+    read as a decode row. is_context_stage, when given, is each row's real
+    stage and decides instead."""
     out = []
-    for f, ql, flag in zip(first_token_indexes, q_lens, is_prefill_requests):
-        out.append(f + ql if flag else f)
+    for b, (f, ql, flag) in enumerate(zip(first_token_indexes, q_lens, is_prefill_requests)):
+        if is_context_stage is not None:
+            decode = not is_context_stage[b]
+        elif use_tensor_cores:
+            decode = (not flag) or (ql == 1 and f > 0)
+        else:
+            decode = not flag
+        out.append(f if decode else f + ql)
     return np.asarray(out, dtype=np.int64)
 
 
@@ -244,3 +261,37 @@ def kept_page_id(base_page: int, num_base_pages_fused: int, fusion_size: int,
     """free_blocks_into_fusion_except: a stale request keeps fused id
     (P_fused // fusion_size) * rank + b (kunserve/block_manager.py:755-760)."""
     return num_base_pages_fused // fusion_size * fusion_rank + base_page
+
+
+def fused_slab(fused_id: int, local_layer: int, base_pages: int, fusion_size: int,
+               num_layers: int) -> tuple[int, int]:
+    """(page, layer) of the unfused [pages, num_layers, ...] pool that fused
+    page `fused_id` uses for layer `local_layer` of its stage.
+
+    Base ids (< P * N): convert_to_pipeline_format splits free page b into
+    fused ids i * P + b (kunserve/block_manager.py:250-253), one per stage of
+    G = num_layers / N layers, and a stale request of rank r keeps r * P + b
+    with its KV still in place (kunserve/block_manager.py:755-760): fused
+    id i * P + b is layers [i * G, (i + 1) * G) of page b. Extend ids
+    (>= P * N, kunserve/block_manager.py:262-269) are G-layer pages carved
+    from the pages behind the base ones (the dropped weight memory), N per
+    page, in order: that layout is inside the absent native LlamaOp, so it
+    is this build's convention, pinned only by the invariants the tests
+    check (disjoint from the base pages, every slab used once)."""
+    g = num_layers // fusion_size
+    if fused_id < base_pages * fusion_size:
+        return fused_id % base_pages, (fused_id // base_pages) * g + local_layer
+    e = fused_id - base_pages * fusion_size
+    return base_pages + e // fusion_size, (e % fusion_size) * g + local_layer
+
+
+def fused_pool_copy(pool: np.ndarray, base_pages: int, fusion_size: int) -> np.ndarray:
+    """The pool as the fused id space sees it: [P*N + E, G, Hkv, ps, D], slab
+    by slab through fused_slab (an element loop over pages and layers)."""
+    pages, layers = pool.shape[:2]
+    g = layers // fusion_size
+    out = np.empty((pages * fusion_size, g) + pool.shape[2:], dtype=pool.dtype)
+    for f in range(pages * fusion_size):
+        for j in range(g):
+            out[f, j] = pool[fused_slab(f, j, base_pages, fusion_size, layers)]
+    return out

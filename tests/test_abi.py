@@ -233,3 +233,55 @@ def test_prefill_plan_properties(rows, heads, num_cus):
     q_indptr = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
     info, items, merges = _prefill_plan(q_indptr, kv, hq, hkv, num_cus)
     _check_prefill_plan(q_indptr, q_lens, kv, hq, hkv, info, items, merges)
+
+
+# ------------------------------------------------------------------------
+# Fused page-id space (host-only entry points).
+
+def _desc(num_pages, layers, heads=2, ps=16, d=128, page_stride=None, layer_stride=None):
+    slab = heads * ps * d
+    ls = slab if layer_stride is None else layer_stride
+    return _lib.KVPool(1 << 20, 2 << 20, num_pages, layers * ls if page_stride is None
+                       else page_stride, ls, ps * d, d, layers, heads, ps, d, _lib.DTYPE_F16)
+
+
+@pytest.mark.parametrize("P,N,L,X", [(4, 2, 4, 3), (6, 4, 8, 2), (5, 1, 2, 0), (3, 8, 8, 1)])
+def test_fused_pool_and_ids_match_the_oracle_map(P, N, L, X):
+    """Page f of the fused pool, local layer j, lies where the oracle's
+    fused_slab says the fused id's slab lies in the unfused pool."""
+    from oracle import paged_attention_ref as ref
+
+    pool = _desc(P + X, L)
+    fused = _lib.KVPool()
+    _lib.call("kunserve_fused_pool", ctypes.byref(pool), P, N, ctypes.byref(fused))
+    G = L // N
+    assert (fused.num_pages, fused.num_layers) == ((P + X) * N, G)
+    assert (fused.k, fused.v, fused.layer_stride, fused.head_stride, fused.token_stride) == \
+        (pool.k, pool.v, pool.layer_stride, pool.head_stride, pool.token_stride)
+    ids = np.arange((P + X) * N, dtype=np.int32)
+    pages = np.empty_like(ids)
+    _lib.call("kunserve_fused_page_ids", ids.ctypes.data, ids.size, P, N, ids.size,
+              pages.ctypes.data)
+    for f, page in zip(ids.tolist(), pages.tolist()):
+        for j in range(G):
+            got = page * fused.page_stride + j * fused.layer_stride
+            b, layer = ref.fused_slab(f, j, P, N, L)
+            assert got == b * pool.page_stride + layer * pool.layer_stride
+
+
+def test_fused_helpers_reject_what_they_cannot_map():
+    fused = _lib.KVPool()
+    layer_major = _desc(8, 4, page_stride=2 * 16 * 128, layer_stride=8 * 2 * 16 * 128)
+    with pytest.raises(_lib.KunserveError) as e:
+        _lib.call("kunserve_fused_pool", ctypes.byref(layer_major), 8, 2, ctypes.byref(fused))
+    assert e.value.code == _lib.EUNSUPPORTED
+    with pytest.raises(_lib.KunserveError, match="equal stages"):
+        _lib.call("kunserve_fused_pool", ctypes.byref(_desc(8, 6)), 8, 4, ctypes.byref(fused))
+    ids = np.array([0, 17], dtype=np.int32)
+    out = np.empty_like(ids)
+    with pytest.raises(_lib.KunserveError) as e:
+        _lib.call("kunserve_fused_page_ids", ids.ctypes.data, 2, 8, 2, 17, out.ctypes.data)
+    assert e.value.code == _lib.ERANGE
+    ids[1] = -1
+    with pytest.raises(_lib.KunserveError):
+        _lib.call("kunserve_fused_page_ids", ids.ctypes.data, 2, 8, 2, 17, out.ctypes.data)

@@ -222,18 +222,28 @@ def test_pack_scatter_round_trip(device):
 
 def test_llama_op_exchange_loopback(device):
     """Two LlamaOps on one GPU: instance A packs its stale pages, instance B
-    scatters them into fused ids — the single-GPU halves of kv_exchange."""
+    (stage 1 of a 2-instance group) scatters them into its fused ids — the
+    single-GPU halves of kv_exchange. Fused id 1*P + b is layers [2, 4) of
+    B's page b (the oracle's fused map)."""
     a = LlamaOp(32, 4, 4, 2, 16, 128, 1, 1, 1, 1, 1, 1, device)
     b = LlamaOp(32, 4, 4, 2, 16, 128, 1, 1, 1, 1, 1, 1, device)
     a.pool.k.copy_(unique_pool(a.pool.k.shape, device))
     a.pool.v.copy_(unique_pool(a.pool.v.shape, device, 8))
-    src = sorted([9, 2, 13])          # pre-fusion ids < P = 16
-    fused = [ref.kept_page_id(p, 32, 2, 1) for p in src]   # rank 1 of a 2-way fusion
+    b.pool.k.zero_()
+    b.pool.v.zero_()
+    b.pmm_drop(1, 2)
+    src = sorted([9, 2, 13])          # pre-fusion ids < P = 32
+    fused = [ref.kept_page_id(p, 64, 2, 1) for p in (20, 5, 31)]
     scr = a.kv_exchange_pack(src, 2, 4)
     b.kv_exchange_scatter(fused, 2, 4, scr)
     torch.cuda.synchronize()
+    bk = ref.fused_pool_copy(b.pool.k.cpu().numpy(), 32, 2)
+    bv = ref.fused_pool_copy(b.pool.v.cpu().numpy(), 32, 2)
     for s, d in zip(src, fused):
-        assert torch.equal(b.pool.k[d, 2:4].view(torch.int16), a.pool.k[s, 2:4].view(torch.int16))
+        assert np.array_equal(bk[d].view(np.int16), a.pool.k[s, 2:4].cpu().numpy().view(np.int16))
+        assert np.array_equal(bv[d].view(np.int16), a.pool.v[s, 2:4].cpu().numpy().view(np.int16))
+    for page, layer in [(20, 0), (20, 1), (5, 0), (31, 1)]:   # the other layer group is untouched
+        assert not b.pool.k[page, layer].view(torch.int16).any()
     a.kv_exchange([[1], [2]], 0, 1, 0, 1, 32, 0)      # group of one: no-op
     with pytest.raises(NotImplementedError):
         a.kv_exchange([[1], [2]], 0, 1, 0, 2, 32, 0)

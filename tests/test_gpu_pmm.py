@@ -165,8 +165,10 @@ def test_llama_op_pmm_drop_and_restore(device):
     for t in (op.pool.k, op.pool.v):
         t.copy_(torch.randn(t.shape, generator=g, device=device).half())
 
-    assert op.pmm_drop(0, 2) == 4             # layers 2 and 3, 2 blocks each
+    # layers 2 and 3, 2 blocks each, counted as the 2-layer blocks of the fused stage
+    assert op.pmm_drop(0, 2) == 8
     assert op.dropped_layers() == [2, 3] and op.max_num_pages == base + 4
+    assert op.num_fused_pages(2) == 2 * base + 8
     kb, vb = bytes_of(op.pool.k), bytes_of(op.pool.v)
     for i, layer in enumerate((2, 3)):
         ids = slice(base + 2 * i, base + 2 * i + 2)
@@ -182,20 +184,26 @@ def test_llama_op_pmm_drop_and_restore(device):
                                        device=device).half())
     op.pool.v[base:].copy_(torch.randn(op.pool.v[base:].shape, generator=g,
                                        device=device).half())
+    # stage 0 of the group runs layers [0, 2) over fused ids: extend ids from 2 * base
+    fused_ext = 2 * base
     q_lens, first, flags = [1, 20], [30, 12], [0, 1]
-    pages = [[base + 1, 4], [base + 3, base + 2]]
-    step = op.pforward(2, 21, op.max_num_pages, 0, 2, [[0] * n for n in q_lens], first, flags,
-                       pages)
+    pages = [[fused_ext + 1, 4], [fused_ext + 7, fused_ext + 2]]
+    step = op.pforward(2, 21, op.num_fused_pages(2), 0, 2, [[0] * n for n in q_lens], first,
+                       flags, pages)
     q = random_tensor((21, 8, 128), device, 31)
     k = random_tensor((21, 2, 128), device, 32)
     v = random_tensor((21, 2, 128), device, 33)
-    kh, vh = op.pool.k.cpu().numpy(), op.pool.v.cpu().numpy()
+    kh = ref.fused_pool_copy(op.pool.k.cpu().numpy(), base, 2)
+    vh = ref.fused_pool_copy(op.pool.v.cpu().numpy(), base, 2)
     out = step.run(0, q, k, v)
     torch.cuda.synchronize()
     kv = np.array([30, 32])
     q_indptr = np.array([0, 1, 21])
-    indptr, indices = step.table.indptr_host, step.table.indices_host
+    indptr = np.array([0, 2, 4])
+    indices = np.array([fused_ext + 1, 4, fused_ext + 7, fused_ext + 2])
     ref.append_kv(kh, vh, 0, indptr, indices, kv, q_indptr, k.cpu().numpy(), v.cpu().numpy())
+    assert np.array_equal(ref.fused_pool_copy(op.pool.k.cpu().numpy(), base, 2).view(np.int16),
+                          kh.view(np.int16))
     want = ref.prefill_attention(q.cpu().numpy(), q_indptr, kh, vh, 0, indptr, indices, kv,
                                  1 / math.sqrt(128))
     assert max_abs(out, want) <= ATOL
@@ -207,7 +215,7 @@ def test_llama_op_pmm_drop_and_restore(device):
     for layer in (0, 1):
         assert torch.equal(op.layer_weights(layer, nbytes).cpu(), host[layer])
     with pytest.raises(ValueError, match="exceeds the pool"):
-        op.pforward(2, 21, base + 4, 0, 2, [[0] * n for n in q_lens], first, flags, pages)
+        op.pforward(2, 21, 2 * base + 8, 0, 2, [[0] * n for n in q_lens], first, flags, pages)
     with pytest.raises(IndexError):
-        op.pforward(2, 21, base, 0, 2, [[0] * n for n in q_lens], first, flags, pages)
+        op.pforward(2, 21, 2 * base, 0, 2, [[0] * n for n in q_lens], first, flags, pages)
     op.pmm.close()

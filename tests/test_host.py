@@ -15,10 +15,30 @@ def test_kv_lens_rule_matches_oracle():
     ql = np.where(flag == 0, 1, ql)
     got = kv_lens_for_step(first, ql, flag)
     assert np.array_equal(got, ref.kv_lens_for_step(first, ql, flag))
-    # use_tensor_cores flags every row as prefill (kunserve/request.py:667-670)
-    assert np.array_equal(kv_lens_for_step([9], [1], [1]), [10])
     with pytest.raises(ValueError):
         kv_lens_for_step([0], [3], [0])
+
+
+def test_kv_lens_with_tensor_cores():
+    """use_tensor_cores flags every row as prefill (kunserve/request.py:667-670).
+    A decode row (first = prompt_len + output_len) keeps kv_len = first, so
+    its token lands at first - 1 and stays inside ceil(first / bs) blocks
+    (kunserve/block_manager.py:493-500); chunks of several tokens and a
+    one-token prompt are prefill. The positions every row writes over whole
+    request lifecycles are checked in test_oracle.py."""
+    rng = np.random.default_rng(1)
+    first = rng.integers(0, 5000, 200)
+    ql = np.where(rng.random(200) < 0.5, 1, rng.integers(2, 600, 200))
+    flag = np.ones(200, dtype=np.int64)
+    got = kv_lens_for_step(first, ql, flag, use_tensor_cores=True)
+    assert np.array_equal(got, ref.kv_lens_for_step(first, ql, flag, use_tensor_cores=True))
+    assert kv_lens_for_step([64], [1], [1], use_tensor_cores=True).tolist() == [64]
+    assert kv_lens_for_step([0], [1], [1], use_tensor_cores=True).tolist() == [1]
+    assert kv_lens_for_step([64], [7], [1], use_tensor_cores=True).tolist() == [71]
+    # the rows' real stages decide when given
+    assert kv_lens_for_step([64], [1], [1], True, is_context_stage=[1]).tolist() == [65]
+    with pytest.raises(ValueError, match="exactly one"):
+        kv_lens_for_step([64], [5], [1], True, is_context_stage=[0])
 
 
 def test_csr_truncates_and_validates():

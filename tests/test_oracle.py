@@ -16,6 +16,8 @@ import torch.nn.functional as F
 
 from oracle import paged_attention_ref as ref
 
+from lifecycle import Request
+
 
 def scatter_dense(dense_k, dense_v, num_pages, num_layers, layer, page_size, rng):
     """Writes per-sequence dense K/V [Hkv, n, D] into random pages with an
@@ -202,48 +204,60 @@ def test_copy_swap_pack_scatter_match_element_loops():
     assert not k2[:, 0].any()
 
 
-class _Request:
-    """Lifecycle of a request restated from kunserve/request.py:368-462:
-    chunked prefill advances prefill_[begin|end]_index; after the prompt each
-    step decodes one token."""
-
-    def __init__(self, prompt_len, chunk):
-        self.prompt_len, self.chunk = prompt_len, chunk
-        self.begin = self.end = 0
-        self.outputs = 0
-
-    def context_stage(self):
-        return self.outputs == 0
-
-    def next_step(self):
-        """(first_token_index, q_len, flag, num_tokens for block allocation)."""
-        if self.context_stage():
-            self.begin = self.end
-            self.end = min(self.begin + self.chunk, self.prompt_len)
-            return self.begin, self.end - self.begin, 1, self.end
-
-    def finish_step(self):
-        if self.context_stage() and self.end < self.prompt_len:
-            return
-        self.outputs += 1
+def _run_lifecycle(kv_rule, prompt_len, chunk, steps, use_tc, page_size=16, real_stage=False):
+    """Positions appended over a request's life with kv_len from kv_rule;
+    asserts every append stays inside the pages the table holds."""
+    req = Request(prompt_len, chunk)
+    positions = []
+    for _ in range(steps):
+        first, ql, flag, ctx, pages = req.step_args(use_tc, page_size)
+        kv = int(kv_rule([first], [ql], [flag], use_tc, [ctx] if real_stage else None)[0])
+        assert kv <= pages * page_size, (first, ql, kv, pages)
+        positions.extend(range(kv - ql, kv))
+        req.finish_step()
+    return positions
 
 
 def test_kv_len_rule_against_request_lifecycle():
-    req = _Request(prompt_len=37, chunk=16)
-    positions = []
-    for _ in range(8):
-        if req.context_stage():
-            first, ql, flag, _ = req.next_step()
-        else:
-            first, ql, flag = req.prompt_len + req.outputs, 1, 0
-        kv = int(ref.kv_lens_for_step([first], [ql], [flag])[0])
-        positions.extend(range(kv - ql, kv))
-        # blocks allocated for the step (kunserve/block_manager.py:493-500) cover kv_len
-        num_tokens = req.end if flag else req.prompt_len + req.outputs
-        assert kv <= num_tokens
-        req.finish_step()
-    # Every token position is appended exactly once, in order.
-    assert positions == list(range(len(positions)))
+    for use_tc in (False, True):
+        pos = _run_lifecycle(ref.kv_lens_for_step, 37, 16, 8, use_tc)
+        # Every token position is appended exactly once, in order.
+        assert pos == list(range(len(pos)))
+
+
+def test_kv_len_rule_with_tensor_cores_over_random_lifecycles():
+    """--use-tensor-cores flags every row as prefill (request.py:667-670):
+    over random prompts and chunk sizes, every position is still appended
+    exactly once and inside the blocks the table holds, for the oracle and
+    for the library's rule alike."""
+    from kunserve_amd import kv_lens_for_step as lib_rule
+
+    rng = np.random.default_rng(11)
+    for _ in range(300):
+        chunk = int(rng.integers(2, 80))
+        prompt = int(rng.integers(1, 400))
+        if prompt > 1 and prompt % chunk == 1:
+            prompt += 1          # a one-token tail chunk: see the next test
+        for rule in (ref.kv_lens_for_step, lib_rule):
+            for ps in (4, 16):
+                pos = _run_lifecycle(rule, prompt, chunk, 12, True, ps)
+                assert pos == list(range(len(pos)))
+
+
+def test_one_token_tail_chunk_needs_the_real_stage():
+    """A prompt one token longer than a chunk multiple ends in a one-token
+    chunk at first index > 0, which the all-prefill flags cannot tell from a
+    decode row; given the rows' real stages the rule appends every position
+    once. A one-token prompt (first index 0) needs no help."""
+    from kunserve_amd import kv_lens_for_step as lib_rule
+
+    for rule in (ref.kv_lens_for_step, lib_rule):
+        pos = _run_lifecycle(rule, 33, 16, 6, True, real_stage=True)
+        assert pos == list(range(len(pos)))
+        pos = _run_lifecycle(rule, 1, 16, 5, True)
+        assert pos == list(range(len(pos)))
+        with pytest.raises(AssertionError):
+            assert _run_lifecycle(rule, 33, 16, 6, True) == list(range(37))
 
 
 def test_fused_page_ids():
@@ -254,6 +268,51 @@ def test_fused_page_ids():
     assert ref.kept_page_id(3, 12, 3, 2) == 11
     # the kept id is one of the fused ids of that page
     assert ref.kept_page_id(3, 12, 3, 2) in ref.fused_page_ids(3, 4, 3)
+
+
+@pytest.mark.parametrize("P,N,L,X", [(4, 2, 4, 3), (5, 4, 8, 2), (3, 1, 2, 1), (7, 8, 8, 0)])
+def test_fused_slab_map_invariants(P, N, L, X):
+    """The fused address map of the oracle, pinned by what the reference's
+    block manager relies on:
+    * a stale request of rank r keeps fused id r*P + b and its KV is not
+      moved (kunserve/block_manager.py:755-760): local layer j of that id is
+      model layer r*G + j of page b;
+    * the fused ids convert_to_pipeline_format makes of free page b
+      (:250-253) cover exactly the L layers of page b, and no other page;
+    * extend ids (:262-269) address only the pages behind the base ones;
+    * every slab of the pool is used by exactly one (fused id, local layer)."""
+    G = L // N
+    seen = {}
+    for f in range((P + X) * N):
+        for j in range(G):
+            slab = ref.fused_slab(f, j, P, N, L)
+            assert slab not in seen, f"slab {slab} used by {seen[slab]} and {(f, j)}"
+            seen[slab] = (f, j)
+    assert set(seen) == {(b, layer) for b in range(P + X) for layer in range(L)}
+    for b in range(P):
+        for r in range(N):
+            kept = ref.kept_page_id(b, P * N, N, r)
+            assert [ref.fused_slab(kept, j, P, N, L) for j in range(G)] == \
+                [(b, r * G + j) for j in range(G)]
+        slabs = {ref.fused_slab(f, j, P, N, L) for f in ref.fused_page_ids(b, P, N)
+                 for j in range(G)}
+        assert slabs == {(b, layer) for layer in range(L)}
+    for f in ref.extend_page_ids(P * N, X * N):
+        assert all(ref.fused_slab(f, j, P, N, L)[0] >= P for j in range(G))
+
+
+def test_fused_pool_copy_is_an_element_loop_of_the_map():
+    rng = np.random.default_rng(7)
+    P, N, L, X = 3, 2, 4, 2
+    pool = rng.permutation((P + X) * L * 2 * 4 * 8).reshape(P + X, L, 2, 4, 8)
+    fused = ref.fused_pool_copy(pool, P, N)
+    assert fused.shape == ((P + X) * N, L // N, 2, 4, 8)
+    for f in range((P + X) * N):
+        for j in range(L // N):
+            page, layer = ref.fused_slab(f, j, P, N, L)
+            for h in range(2):
+                for t in range(4):
+                    assert np.array_equal(fused[f, j, h, t], pool[page, layer, h, t])
 
 
 # ------------------------------------------------------------------ rope
