@@ -229,6 +229,25 @@ int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer,
                           void* workspace_dev, int64_t workspace_bytes,
                           kunserve_stream_t stream);
 
+/* kunserve_paged_decode without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The split partials live in a static device array of
+ * kunserve_paged_decode_noalloc_max_bytes() (32 MiB) that each device the
+ * library runs on holds until the process ends; plans whose
+ * kunserve_decode_workspace_bytes exceed it fail with KUNSERVE_ENOSPC. The
+ * call allocates nothing. Every call on one device shares that array:
+ * calls that overlap on one device (concurrent streams) race, so serialise
+ * them. Results equal kunserve_paged_decode's bit for bit. */
+int64_t kunserve_paged_decode_noalloc_max_bytes(void);
+int kunserve_paged_decode_noalloc(const kunserve_kv_pool* pool, int32_t layer,
+                                  const kunserve_page_table* table,
+                                  const kunserve_tensor3* q, kunserve_tensor3* out,
+                                  int32_t num_qo_heads, float sm_scale,
+                                  const int32_t* plan_dev,
+                                  const kunserve_decode_plan_info* info,
+                                  kunserve_stream_t stream);
+
 /* ------------------------------------- chunked-prefill attention (A5 ii) */
 
 typedef struct {

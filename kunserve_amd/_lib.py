@@ -85,6 +85,11 @@ SIGNATURES = {
                                       POINTER(Tensor3), POINTER(Tensor3), c_int32, c_float,
                                       c_void_p, POINTER(DecodePlanInfo), c_void_p, c_int64,
                                       c_void_p]),
+    "kunserve_paged_decode_noalloc_max_bytes": (c_int64, []),
+    "kunserve_paged_decode_noalloc": (c_int, [POINTER(KVPool), c_int32, POINTER(PageTable),
+                                              POINTER(Tensor3), POINTER(Tensor3), c_int32,
+                                              c_float, c_void_p, POINTER(DecodePlanInfo),
+                                              c_void_p]),
     "kunserve_prefill_plan_bound": (c_int64, [c_void_p, c_int32, c_int32]),
     "kunserve_prefill_plan": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
                                       c_void_p, c_int64, POINTER(PrefillPlanInfo)]),

@@ -23,6 +23,7 @@
 //    their log-sum-exp (base 2); a small merge kernel combines them.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "common.hpp"
@@ -795,4 +796,84 @@ extern "C" int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer
   if (pool->dtype == KUNSERVE_DTYPE_BF16)
     return run_decode<bf16>(a, *info, plan_dev, pool->head_dim, num_qo_heads, grid, s);
   return run_decode<f16>(a, *info, plan_dev, pool->head_dim, num_qo_heads, grid, s);
+}
+
+// ------------------------------------------------ decode without allocation
+// kunserve_paged_decode_noalloc keeps the split partials in `scratch`, a
+// file-scope device array of kNoAllocScratchBytes that every device the
+// library runs on holds until the process ends. In host code `scratch` is
+// only a stand-in for the symbol: its device address, one per device, comes
+// from hipGetSymbolAddress with that device current, and only that address
+// is ever handed to a kernel.
+namespace kunserve {
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mutex;
+std::vector<void*> g_scratch_ptr;   // by device ordinal
+
+// Device address of `scratch` on `device`, looked up once per device.
+int scratch_address(int device, void** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (device >= int(g_scratch_ptr.size())) g_scratch_ptr.resize(device + 1, nullptr);
+  if (!g_scratch_ptr[device]) {
+    int current = 0;
+    KSV_CHECK_HIP(hipGetDevice(&current));
+    if (current != device) KSV_CHECK_HIP(hipSetDevice(device));
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (current != device) KSV_CHECK_HIP(hipSetDevice(current));
+    if (e != hipSuccess || !ptr) {
+      set_error("hipGetSymbolAddress(scratch) on device %d failed: %s", device,
+                hipGetErrorString(e));
+      return KUNSERVE_EHIP;
+    }
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return KUNSERVE_OK;
+}
+
+}  // namespace
+}  // namespace kunserve
+
+extern "C" int64_t kunserve_paged_decode_noalloc_max_bytes(void) {
+  return kunserve::kNoAllocScratchBytes;
+}
+
+extern "C" int kunserve_paged_decode_noalloc(const kunserve_kv_pool* pool, int32_t layer,
+                                             const kunserve_page_table* table,
+                                             const kunserve_tensor3* q, kunserve_tensor3* out,
+                                             int32_t num_qo_heads, float sm_scale,
+                                             const int32_t* plan_dev,
+                                             const kunserve_decode_plan_info* info,
+                                             kunserve_stream_t stream) {
+  using namespace kunserve;
+  clear_error();
+  int rc = check_pool(pool, true);
+  if (rc) return rc;
+  KSV_CHECK_ARG(info != nullptr, "null plan info");
+  const int64_t need = kunserve_decode_workspace_bytes(info, num_qo_heads, pool->head_dim);
+  KSV_CHECK_ARG(need >= 0, "bad plan or head counts");
+  if (need > kNoAllocScratchBytes) {
+    set_error("decode partials need %lld bytes, more than the %lld bytes of the static "
+              "scratch of kunserve_paged_decode_noalloc; use kunserve_paged_decode with a "
+              "workspace", (long long)need, (long long)kNoAllocScratchBytes);
+    return KUNSERVE_ENOSPC;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    int device = 0;
+    if (stream) {
+      KSV_CHECK_HIP(hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &device));
+    } else {
+      KSV_CHECK_HIP(hipGetDevice(&device));
+    }
+    rc = scratch_address(device, &ws);
+    if (rc) return rc;
+  }
+  return kunserve_paged_decode(pool, layer, table, q, out, num_qo_heads, sm_scale, plan_dev, info,
+                               ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
 }
