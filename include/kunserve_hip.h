@@ -131,6 +131,14 @@ int kunserve_kv_scatter(const kunserve_kv_pool* pool, int32_t layer_begin,
 int64_t kunserve_kv_pack_bytes(const kunserve_kv_pool* pool, int32_t num_layers,
                                int64_t n);
 
+/* Bandwidth calibration (no reference counterpart): streams `bytes` (a
+ * multiple of 256 KiB) with the launch shape of the block copy. mode 0
+ * reads src_dev only (dst_dev must hold 16 bytes), mode 1 writes dst_dev
+ * only, mode 2 copies src_dev to dst_dev. The benchmark times these to
+ * give the block copy's ceiling on the part it runs on. */
+int kunserve_hbm_probe(int32_t mode, const void* src_dev, void* dst_dev,
+                       int64_t bytes, kunserve_stream_t stream);
+
 /* ------------------------------------------------------------ swap (A7) */
 
 /* torch.ops.swapping_ops.swap (kunserve/worker.py:646-650,673-681):

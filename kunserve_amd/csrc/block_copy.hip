@@ -413,3 +413,80 @@ extern "C" int kunserve_swap_blocks(const int64_t* src_ids_host, const int64_t* 
   }
   return KUNSERVE_OK;
 }
+
+// ------------------------------------------------- bandwidth calibration
+// Flat streams with the launch shape of the large-span copy above (1024
+// threads, 256 KiB per workgroup, eight 16-byte non-temporal accesses in
+// flight per lane): reading only, writing only, and copying. They measure
+// what this part's HBM gives each access mix, the ceiling the block copy is
+// judged against.
+namespace kunserve {
+namespace {
+
+constexpr int kProbeThreads = kLargeThreads;
+constexpr int64_t kProbeChunk = chunk_bytes(kLargeThreads, kLargeRounds);
+
+template <int MODE>   // 0 read, 1 write, 2 copy
+__global__ __launch_bounds__(kProbeThreads) void hbm_probe_kernel(const char* src, char* dst) {
+  constexpr int32_t kRound = kProbeThreads * 16 * kUnroll;
+  const int64_t base = int64_t(blockIdx.x) * kProbeChunk + int32_t(threadIdx.x) * 16;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+#pragma unroll 1
+  for (int r = 0; r < kLargeRounds; ++r) {
+    u32x4 buf[kUnroll];
+    if constexpr (MODE != 1) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+        buf[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(src + base + r * kRound + u * kProbeThreads * 16));
+    } else {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+        buf[u] = u32x4{uint32_t(base), uint32_t(r), uint32_t(u), 0x5a5a5a5au};
+    }
+    if constexpr (MODE == 0) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) acc ^= buf[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+        __builtin_nontemporal_store(
+            buf[u], reinterpret_cast<u32x4*>(dst + base + r * kRound + u * kProbeThreads * 16));
+    }
+  }
+  if constexpr (MODE == 0) {
+    // Keeps the loads alive; the pattern cannot come from the caller's data
+    // except by accident, and then only one 16-byte slot is written.
+    if (acc[0] == 0x9e3779b9u && acc[1] == 0x7f4a7c15u && acc[2] == 0xf39cc060u &&
+        acc[3] == 0x5851f42du)
+      *reinterpret_cast<u32x4*>(dst) = acc;
+  }
+}
+
+}  // namespace
+}  // namespace kunserve
+
+extern "C" int kunserve_hbm_probe(int32_t mode, const void* src_dev, void* dst_dev, int64_t bytes,
+                                  kunserve_stream_t stream) {
+  using namespace kunserve;
+  clear_error();
+  KSV_CHECK_ARG(mode >= 0 && mode <= 2, "mode %d is not 0 (read), 1 (write) or 2 (copy)", mode);
+  KSV_CHECK_ARG(bytes > 0 && bytes % kProbeChunk == 0, "bytes must be a positive multiple of %lld",
+                (long long)kProbeChunk);
+  KSV_CHECK_ARG(dst_dev && aligned16(dst_dev) && (mode == 1 || (src_dev && aligned16(src_dev))),
+                "null or misaligned buffer");
+  const int64_t blocks = bytes / kProbeChunk;
+  KSV_CHECK_ARG(blocks < (int64_t(1) << 31), "too many bytes for one launch");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const char* src = static_cast<const char*>(src_dev);
+  char* dst = static_cast<char*>(dst_dev);
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (mode == 0)
+    hbm_probe_kernel<0><<<grid, kProbeThreads, 0, s>>>(src, dst);
+  else if (mode == 1)
+    hbm_probe_kernel<1><<<grid, kProbeThreads, 0, s>>>(src, dst);
+  else
+    hbm_probe_kernel<2><<<grid, kProbeThreads, 0, s>>>(src, dst);
+  KSV_CHECK_LAUNCH();
+  return KUNSERVE_OK;
+}

@@ -402,3 +402,24 @@ def test_rope_append_positions_and_pages():
         page = indices[indptr[b] + pos[t] // ps]
         np.testing.assert_array_equal(k_pool[page, 0, :, pos[t] % ps], kr[t])
         np.testing.assert_array_equal(v_pool[page, 0, :, pos[t] % ps], vn[t])
+
+
+def test_torch_cpu_restatement_matches_the_oracle():
+    """The PyTorch-CPU decode that bench.py times as its CPU baseline computes
+    the oracle's decode (fp32 vs float64: within 1e-5 on fp16 pages)."""
+    from oracle import torch_cpu
+
+    rng = np.random.default_rng(17)
+    npg, L, hkv, ps, d = 40, 2, 4, 16, 64
+    for hq in (4, 16):
+        k = rng.standard_normal((npg, L, hkv, ps, d)).astype(np.float16)
+        v = rng.standard_normal((npg, L, hkv, ps, d)).astype(np.float16)
+        kv = np.array([0, 1, 17, 200, 96])
+        need = (kv + ps - 1) // ps
+        indptr = np.concatenate([[0], np.cumsum(need)])
+        indices = rng.permutation(npg)[:indptr[-1]]
+        q = rng.standard_normal((5, hq, d)).astype(np.float16)
+        want = ref.decode_attention(q, k, v, 1, indptr, indices, kv, 0.125)
+        got = torch_cpu.decode_attention(torch.from_numpy(q), torch.from_numpy(k),
+                                         torch.from_numpy(v), 1, indptr, indices, kv, 0.125)
+        np.testing.assert_allclose(got.numpy(), want, rtol=0, atol=1e-5)
