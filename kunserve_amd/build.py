@@ -32,6 +32,19 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions. The one-wave-per-SIMD prefill kernel keeps its
+# score accumulators in VGPRs, where its softmax reads them; with the
+# default AGPR form the register allocator shuffles them between the two
+# register files at every phase.
+EXTRA_FLAGS = {
+    "paged_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
+def flags_for(src: Path) -> list[str]:
+    return [*HIPCC_FLAGS, *EXTRA_FLAGS.get(Path(src).name, [])]
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -45,7 +58,7 @@ def sources() -> list[Path]:
 
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *flags_for(src), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature.
     err = "\n".join(

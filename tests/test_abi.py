@@ -144,20 +144,21 @@ def test_prefill_plan_covers_every_tile_once(hq, hkv, n):
 @pytest.mark.parametrize("num_cus", [0, 64, 256, 1024])
 def test_prefill_plan_splits_small_steps(num_cus):
     """A step with fewer q-tile items than CUs (one long row: the last step
-    of a chunked prefill, 64 items) is split over about one workgroup per
-    CU; a step with enough items is not."""
+    of a chunked prefill, 32 heads x 512 / tile_q items) is split over about
+    one workgroup per CU; a step with enough items is not."""
     q_lens = np.array([512], dtype=np.int64)
     kv = np.array([4806], dtype=np.int32)
     q_indptr = np.array([0, 512], dtype=np.int32)
     info, items, merges = _prefill_plan(q_indptr, kv, 32, 32, num_cus)
     _check_prefill_plan(q_indptr, q_lens, kv, 32, 32, info, items, merges)
     cus = num_cus or 256
+    n_items = -(-512 // info.tile_q) * 32
     real = int((items[:, 0] >= 0).sum())
-    if cus <= 64:
-        assert info.num_merge == 0 and real == 64
+    if cus <= n_items:
+        assert info.num_merge == 0 and real == n_items
     else:
-        assert info.num_merge == 64 and info.kv_chunk % 64 == 0 and info.kv_chunk >= 256
-        assert 0.75 * cus <= real <= cus + 64
+        assert info.num_merge == n_items and info.kv_chunk % 64 == 0 and info.kv_chunk >= 256
+        assert 0.75 * cus <= real <= cus + n_items
     big = np.full(16, 512, dtype=np.int64)
     qi = np.concatenate([[0], np.cumsum(big)]).astype(np.int32)
     kvb = np.full(16, 2048, dtype=np.int32)

@@ -19,7 +19,7 @@ FORBIDDEN = [
 @pytest.mark.parametrize("src", kb.sources(), ids=lambda p: p.name)
 def test_device_code_has_no_forbidden_instructions(src, tmp_path):
     out = tmp_path / (src.stem + ".s")
-    cmd = [kb.hipcc(), *kb.HIPCC_FLAGS, "--cuda-device-only", "-S", str(src), "-o", str(out)]
+    cmd = [kb.hipcc(), *kb.flags_for(src), "--cuda-device-only", "-S", str(src), "-o", str(out)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     assert proc.returncode == 0, proc.stderr[-2000:]
     asm = out.read_text()
