@@ -32,13 +32,8 @@ HIPCC_FLAGS = [
 ]
 
 
-# Per-source additions. The one-wave-per-SIMD prefill kernel keeps its
-# score accumulators in VGPRs, where its softmax reads them; with the
-# default AGPR form the register allocator shuffles them between the two
-# register files at every phase.
-EXTRA_FLAGS = {
-    "paged_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-}
+# Per-source additions to HIPCC_FLAGS (none at present).
+EXTRA_FLAGS: dict[str, list[str]] = {}
 
 
 def flags_for(src: Path) -> list[str]:

@@ -26,7 +26,6 @@
 //    max, sum) and a merge kernel combines them in split order.
 #include <algorithm>
 #include <cmath>
-#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -36,10 +35,7 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
-// Which attention kernel runs: one wave per SIMD on 128-row tiles, or two
-// waves per SIMD on 256-row tiles. The plan's tiles follow it.
-constexpr bool kPrefillOneWavePerSimd = false;
-constexpr int kTileQ = kPrefillOneWavePerSimd ? 128 : 32 * kWaves;   // query rows per workgroup
+constexpr int kTileQ = 32 * kWaves;   // query rows per workgroup
 constexpr int kTileKV = 64;           // kv tokens per iteration
 constexpr int kD = 128;               // head_dim of the MFMA kernel
 constexpr int kXcds = 8;              // MI355X: workgroup i runs on XCD i % 8
@@ -77,62 +73,57 @@ constexpr int kRec = 6;
 constexpr int kMergeRec = 5;
 
 // LDS layouts; every operand address is a per-lane base plus an immediate
-// offset.
-// K tile: row-major [token][dim], rows 68 dwords apart: an operand read
-//   (16 lanes: 16 consecutive rows, one 16-byte chunk) hits 64 distinct
-//   banks.
-// V tile: transposed, row d holds dim d of the tile's 64 tokens, rows 72
-//   halves apart, so the V^T operands are plain 16-byte reads (the gfx950
+// offset. Bank behaviour was measured on gfx950 with SQ_LDS_BANK_CONFLICT:
+// 8-byte stores go 16 lanes per cycle over 32 banks; the 16-byte accesses
+// below measured conflict-free (16-byte reads follow no simple lane-group
+// model, so layouts were chosen by measurement).
+// K tile: row-major [token][dim], rows 68 dwords apart; operand reads (row
+//   32 mt + r, one 16-byte chunk) and the gather's 16-byte row stores are
+//   conflict-free.
+// V tile: transposed, row d holds dim d of the tile's 64 tokens, rows 128
+//   bytes apart, so the V^T operands are plain 16-byte reads (the gfx950
 //   transposing read, ds_read_b64_tr_b16, moves a quarter of the bytes per
 //   cycle, and every wave reads the whole tile). Columns follow the P^T
 //   operand: within each 16 tokens, token 8a + 4h + b sits at column
 //   8h + 4a + b, so the 8 tokens one lane's operand needs are one 16-byte
-//   chunk. Chunk c of row d is stored at chunk c ^ ((d >> 4) & 7): with the
-//   72-half pitch, the gather's 8-byte stores (32 lanes: 16 dims 8 apart x 2
-//   chunk halves) and the operand's 16-byte reads (16 lanes: 16 consecutive
-//   dims) each hit 64 distinct banks.
+//   chunk. Chunk c of row d is stored at chunk c ^ ((d ^ (d >> 3)) & 7):
+//   conflict-free for both the operand reads and the gather's 8-byte stores
+//   (a store pass, 16 lanes, covers 8 dims 8 apart x both halves of a chunk).
 constexpr int kKPitch = kD + 8;     // halves
 constexpr int kKHalves = kTileKV * kKPitch;
-constexpr int kVtPitch = kTileKV + 8;
+constexpr int kVtPitch = kTileKV;   // halves
 constexpr int kVtHalves = kD * kVtPitch;
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Gather layout of both kernels: lane l of a gathering wave with token
-// group g (0..3) moves dims 8 (l % 16) .. +8 of the 4 consecutive tokens
-// gather_token(g, l) + i, i < 4; a load round reads 4 whole 256-byte rows
-// per wave. The tokens are 4-aligned, so (page_size >= 4) one page holds
-// them.
+// Gather layout: lane l of a gathering wave with token group g (0..3) moves
+// dims 8 c .. +8, c = (l & 7) | ((l >> 4) & 1) << 3, of the 4 consecutive
+// tokens gather_token(g, l) + i, i < 4; a load round reads 4 whole 256-byte
+// rows per wave (lanes 8 apart cover a row's halves). The tokens are
+// 4-aligned, so (page_size >= 4) one page holds them.
 __device__ __forceinline__ int gather_token(int g, int lane) {
-  return 16 * g + 8 * ((lane >> 4) & 1) + 4 * (lane >> 5);
+  return 16 * g + 8 * ((lane >> 3) & 1) + 4 * (lane >> 5);
 }
-__device__ __forceinline__ int gather_dim(int lane) { return (lane & 15) * 8; }
-// Offset (halves) in a V^T buffer of the gathering lane's 8-byte store of
-// dim gather_dim + e: add e * kVtPitch.
-__device__ __forceinline__ int vt_store_base(int g, int lane) {
-  const int c = lane & 15, a = (lane >> 4) & 1, h = lane >> 5;
-  return 8 * c * kVtPitch + 8 * ((2 * g + h) ^ (c >> 1)) + 4 * a;
-}
-// Offset (halves) in a V^T buffer of the lane's operand (ks = 0, dt = 0):
-// row d = 32 dt + r, logical chunk 2 ks + h is stored at chunk
-// (2 ks + h) ^ (2 dt + r / 16) = 2 (ks ^ dt) + (h ^ r / 16).
-__device__ __forceinline__ int vt_operand_base(int lane) {
-  const int r = lane & 31, h = lane >> 5;
-  return r * kVtPitch + 8 * (h ^ (r >> 4));
-}
-__device__ __forceinline__ int vt_operand(int ks, int dt) { return 32 * dt * kVtPitch + 16 * (ks ^ dt); }
+__device__ __forceinline__ int gather_chunk(int lane) { return (lane & 7) | (((lane >> 4) & 1) << 3); }
+__device__ __forceinline__ int gather_dim(int lane) { return 8 * gather_chunk(lane); }
 
-// Transposed store of dims 2 part, 2 part + 1 of a lane's 4 tokens (x[i]:
-// token i, 8 dims) at dst (buffer + vt_store_base). v_perm builds each
-// dword from two tokens' dwords; its selector byte 0x0c yields a zero byte,
-// which zeroes the tokens from nok on.
+// Transposed store of dims 2 part, 2 part + 1 of a gathering lane's 4
+// tokens (x[i]: token i, 8 dims) into the V^T buffer buf. Dim 8 c + e of
+// token group g is row 8 c + e, logical chunk 2 g + h, stored at chunk
+// (2 g + h) ^ c ^ e (c, e < 8 here), at half 4 a of it. v_perm builds each
+// dword from two tokens' dwords; its selector byte 0x0c yields a zero
+// byte, which zeroes the tokens from nok on.
 template <typename T>
-__device__ __forceinline__ void vt_store(T* dst, const typename Vec<T>::v8 (&x)[4], int part,
-                                         int nok) {
+__device__ __forceinline__ void vt_store(T* buf, int g, int lane,
+                                         const typename Vec<T>::v8 (&x)[4], int part, int nok) {
+  const int c = gather_chunk(lane), a = (lane >> 3) & 1, h = lane >> 5;
+  const int row0 = 8 * c * kVtPitch + 4 * a;
+  const int chunk0 = (2 * g + h) ^ (c & 7);
   const uint32_t z01 = (nok < 1 ? 0x0000ffffu : 0u) | (nok < 2 ? 0xffff0000u : 0u);
   const uint32_t z23 = (nok < 3 ? 0x0000ffffu : 0u) | (nok < 4 ? 0xffff0000u : 0u);
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
+    const int e = 2 * part + half;
     const uint32_t sel = half ? 0x07060302u : 0x05040100u;   // high / low halves
     const uint32_t s01 = (sel & ~z01) | (0x0c0c0c0cu & z01);
     const uint32_t s23 = (sel & ~z23) | (0x0c0c0c0cu & z23);
@@ -140,9 +131,27 @@ __device__ __forceinline__ void vt_store(T* dst, const typename Vec<T>::v8 (&x)[
                                            __builtin_bit_cast(u32x4, x[0])[part], s01),
                      __builtin_amdgcn_perm(__builtin_bit_cast(u32x4, x[3])[part],
                                            __builtin_bit_cast(u32x4, x[2])[part], s23)};
-    *reinterpret_cast<u32x2*>(dst + (2 * part + half) * kVtPitch) = d;
+    *reinterpret_cast<u32x2*>(buf + row0 + e * kVtPitch + 8 * (chunk0 ^ e)) = d;
   }
 }
+
+// V^T operand (ks, dt) of lane (r, h): row d = 32 dt + r, logical chunk
+// 2 ks + h, stored at chunk (2 ks + h) ^ ((d ^ (d >> 3)) & 7)
+// = (2 ks ^ 4 (dt & 1)) ^ (h ^ (r & 7) ^ (r >> 3)): one of four per-lane
+// bases, j = ks ^ 2 (dt & 1), plus an immediate offset.
+struct VtBases {
+  int b[4];
+};
+__device__ __forceinline__ VtBases vt_operand_bases(int lane) {
+  const int r = lane & 31, h = lane >> 5;
+  const int s = h ^ (r & 7) ^ (r >> 3);
+  VtBases v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v.b[j] = r * kVtPitch + 8 * ((2 * j) ^ s);
+  return v;
+}
+__device__ __forceinline__ int vt_operand_base_index(int ks, int dt) { return ks ^ (2 * (dt & 1)); }
+__device__ __forceinline__ int vt_operand_offset(int dt) { return 32 * dt * kVtPitch; }
 
 // Where a gathering lane's 4 tokens of the tile at kv token tok0 are:
 // element offset in a layer and how many of them hold data (0 on a page id
@@ -282,12 +291,11 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     for (int i = 0; i < 4; ++i) rg.x[i] = load_v8<T>(gbase + at.off + int64_t(i) * a.token_stride);
     rg.nok = at.nok;
   };
-  const int vt_w = vt_store_base(wave & 3, lane);
   auto stash = [&](int buf, const Regs& rg) {
     if (gather_v) {
 #pragma unroll
       for (int part = 0; part < 4; ++part)
-        vt_store<T>(sVt + buf * kVtHalves + vt_w, rg.x, part, rg.nok);
+        vt_store<T>(sVt + buf * kVtHalves, wave & 3, lane, rg.x, part, rg.nok);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -298,11 +306,11 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   // Per-lane LDS bases; each operand read adds a compile-time offset.
   // K A operand (S^T = K.Q^T): row 32 mt + r, dims 16 s + 8 h .. +8.
   const int kb0 = r * kKPitch + 8 * h;
-  const int vb0 = vt_operand_base(lane);
+  const VtBases vb = vt_operand_bases(lane);
 
   auto compute = [&](int buf, int n0) {
     const T* kt = sK + buf * kKHalves + kb0;
-    const T* vt = sVt + buf * kVtHalves + vb0;
+    const T* vt = sVt + buf * kVtHalves;
     // S^T tiles: rows = kv tokens 32*mt + i, columns = query rows.
     f32x16 st[2];
 #pragma unroll
@@ -371,7 +379,8 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const V8 va = *reinterpret_cast<const V8*>(vt + vt_operand(ks, dt));
+        const V8 va = *reinterpret_cast<const V8*>(vt + vb.b[vt_operand_base_index(ks, dt)] +
+                                                    vt_operand_offset(dt));
         o[dt] = mfma32(va, pb[ks], o[dt]);
       }
     }
@@ -442,402 +451,6 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     a.part_ml[2 * prow + 1] = lsum;
   }
 }
-
-// One wave per SIMD: 4 waves of 32 query rows per workgroup (128-row tiles).
-// A wave with its SIMD to itself can overlap its own MFMA and VALU work, but
-// only in its instruction stream (issue is in order), so every iteration is
-// two phases whose MFMAs carry the other work between them (sched_barrier
-// keeps the order):
-//   phase A: S(t+1) = K(t+1).Q^T         | softmax of tile t; stash K(t+2)
-//                                          and V(t+1)
-//   phase B: O += V(t)^T.P(t)^T          | row sums of P(t); issue the loads
-//                                          of K(t+4) and V(t+3)
-// MFMA operands are read from LDS kAhead MFMAs ahead. During iteration t
-// the LDS holds K(t+1) and V(t); K(t+2) and V(t+1) go to the buffers of
-// K(t) and V(t-1), read only in iteration t-1, so one barrier per iteration
-// suffices. The global loads of a gather run two iterations ahead in two
-// register sets.
-constexpr int kW4Threads = 256;
-constexpr int kW4Waves = kW4Threads / kWave;
-static_assert(!kPrefillOneWavePerSimd || kW4Waves * 32 == kTileQ,
-              "four waves of 32 rows make the 128-row tile");
-constexpr int kAhead = 4;   // MFMAs an LDS operand read runs ahead of its use
-constexpr int kW4Loads = kTileKV * kD / 8 / kW4Threads;   // 16-byte K (and V) loads per thread
-static_assert(kW4Loads == 4 && kW4Waves * 16 == kTileKV,
-              "a thread gathers 4 consecutive tokens, a wave 16: one page per thread");
-
-#define KSV_ORDER() __builtin_amdgcn_sched_barrier(0)
-
-// Stash flag of phase A: a bool constant, or nullptr_t for no stash.
-template <typename C> constexpr bool kStashCheck = C::value;
-template <> constexpr bool kStashCheck<std::nullptr_t> = false;
-
-template <typename T, bool STAGED>
-__global__ __launch_bounds__(kW4Threads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void paged_prefill_w4_kernel(PrefillArgs a) {
-  typedef typename Vec<T>::v8 V8;
-  typedef typename Vec<T>::v4 V4;
-  __shared__ int s_pg[STAGED ? kMaxStagedPages : 1];
-  __shared__ int s_bad[kW4Waves];
-  __shared__ __attribute__((aligned(16))) T sK[2 * kKHalves];
-  __shared__ __attribute__((aligned(16))) T sVt[2 * kVtHalves];
-
-  const int32_t* item = a.tiles + kRec * blockIdx.x;
-  const int seq = item[0];
-  if (seq < 0) return;   // padding workgroup (uniform: no barrier reached)
-  const int q0 = item[1];
-  const int hq = item[2];
-  const int kv_lo = item[3];   // a multiple of kTileKV
-  const int kv_hi = item[4];
-  const int slot = item[5];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: phase tests branch on it
-  const int r = lane & 31;       // query row within the wave / MFMA column
-  const int h = lane >> 5;       // MFMA k-half
-
-  const int hkv = hq / a.ratio;
-  const int qb = a.q_indptr[seq];
-  const int q_len = a.q_indptr[seq + 1] - qb;
-  const int kvl = a.kv_len[seq];
-  const int prefix = kvl - q_len;
-  const int32_t* pages = a.indices + a.indptr[seq];
-  const int page_mask = (1 << a.page_shift) - 1;
-
-  const int qrow = q0 + 32 * wave + r;
-  const bool row_ok = qrow < q_len;
-  const int qpos = prefix + qrow;
-  const bool wave_on = q0 + 32 * wave < q_len;
-  const int first_pos = prefix + q0 + 32 * wave;
-  const int last_pos = prefix + min(q0 + 32 * wave + 31, q_len - 1);
-  const int kv_end = min(prefix + min(q0 + kTileQ, q_len), kv_hi);   // exclusive
-  const int j_lo = kv_lo / kTileKV;
-  const int ntiles = (kv_end + kTileKV - 1) / kTileKV;   // tiles [j_lo, ntiles)
-  // Last tile with keys this wave's rows see (j_lo - 1: none in this range).
-  const int j_last = wave_on ? min(last_pos / kTileKV, ntiles - 1) : j_lo - 1;
-  const int pg_lo = kv_lo >> a.page_shift;
-
-  bool any_bad = false;
-  {
-    const int npg = kv_end > kv_lo ? ((kv_end - 1) >> a.page_shift) + 1 - pg_lo : 0;
-    bool bad_id = false;
-    for (int i = tid; i < npg; i += kW4Threads) {
-      const int p = pages[pg_lo + i];
-      const bool ok = p >= 0 && p < a.num_pages;
-      if constexpr (STAGED) s_pg[i] = ok ? p : -1;
-      bad_id |= !ok;
-    }
-    const bool wave_bad = __any(bad_id);
-    if (lane == 0) s_bad[wave] = wave_bad;
-    __syncthreads();
-    int bad = 0;
-#pragma unroll
-    for (int wv = 0; wv < kW4Waves; ++wv) bad |= s_bad[wv];
-    any_bad = __builtin_amdgcn_readfirstlane(bad) != 0;
-  }
-  // Page id of kv token tok, read unconditionally: tok is clamped into the
-  // staged range [kv_lo, kv_end), so callers mask by tok themselves.
-  auto page_of = [&](int tok) __attribute__((always_inline)) {
-    const int t = max(kv_lo, min(tok, kv_end - 1));
-    return STAGED ? s_pg[(t >> a.page_shift) - pg_lo] : pages[t >> a.page_shift];
-  };
-
-  // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
-  V8 qf[8];
-  {
-    const f16* qp = a.q + int64_t(qb + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = row_ok ? load_v8<T>(qp + 16 * s + 8 * h) : V8{};
-  }
-
-  f32x16 o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
-  float m = -1.0e30f;   // running max of this row, in scaled (log2) units
-  float lsum = 0.f;     // this lane's share of the row sum (other half: lane ^ 32)
-
-  const f16* kbase = a.k + int64_t(hkv) * a.head_stride;
-  const f16* vbase = a.v + int64_t(hkv) * a.head_stride;
-
-  // Gather: every wave moves K and V, token group = its wave (gather_token).
-  // A gather unit is K(t + 2) with V(t + 1).
-  const int ld_c = gather_dim(lane);
-  const int ld_t = gather_token(wave, lane);
-  V8 gk[2][kW4Loads], gv[2][kW4Loads];
-  int gv_ok[2];   // tokens of gv[u] that hold data (TileAt::nok)
-  // The page comes from page_of, which clamps into the row. Computed an
-  // iteration before the loads that use it, so no lookup latency sits in
-  // front of them.
-  auto at_tile = [&](int j) __attribute__((always_inline)) {
-    const int tok = j * kTileKV + ld_t;
-    return tile_at(page_of(tok), tok, kv_end, a.num_pages, a.page_stride, a.token_stride,
-                   page_mask, ld_c);
-  };
-  TileAt atk, atv;   // tiles of the next loads of K and of V
-  auto load_tok = [&](const f16* base, const TileAt& at, int i) __attribute__((always_inline)) {
-    return load_v8<T>(base + at.off + int64_t(i) * a.token_stride);
-  };
-  auto put_k = [&](int j, const V8& x, int i) __attribute__((always_inline)) {
-    *reinterpret_cast<V8*>(&sK[(j & 1) * kKHalves + (ld_t + i) * kKPitch + ld_c]) = x;
-  };
-  const int vt_w = vt_store_base(wave, lane);
-  auto put_vt = [&](int j, const V8 (&x)[kW4Loads], int part, int nok) __attribute__((always_inline)) {
-    vt_store<T>(sVt + (j & 1) * kVtHalves + vt_w, x, part, nok);
-  };
-
-  // Per-lane LDS bases. K operand i of the score phase is (mt = i & 1,
-  // s = i >> 1): two independent accumulator chains.
-  const int kb0 = r * kKPitch + 8 * h;
-  const int vb0 = vt_operand_base(lane);
-  auto k_op = [&](const T* kt, int i) __attribute__((always_inline)) {
-    return *reinterpret_cast<const V8*>(kt + 32 * (i & 1) * kKPitch + 16 * (i >> 1));
-  };
-  // V^T operand i of the P.V phase is (ks = i >> 2, dt = i & 3).
-  auto v_op = [&](const T* vt, int i) __attribute__((always_inline)) {
-    return *reinterpret_cast<const V8*>(vt + vt_operand(i >> 2, i & 3));
-  };
-
-  f32x16 sc[2][2];   // S^T of two tiles (rows = tokens 32 mt + i, columns = query rows)
-  V8 pb[4];          // P^T as B operands
-  const V8 ones = {T(1.f), T(1.f), T(1.f), T(1.f), T(1.f), T(1.f), T(1.f), T(1.f)};
-
-  // Phase A: S of tile ts into sc[ns] (do_s) and the softmax of tile tp from
-  // sc[np] (do_p). The max needs every score, so MFMAs 0-3 carry it and the
-  // rescale branch follows them; MFMAs 4-15 carry three exponentials each.
-  auto phase_a = [&](int ns, int ts, auto DO_S, int np, int tp, auto DO_P, int G, int tg,
-                     auto CHECK) __attribute__((always_inline)) {
-    constexpr bool do_s = decltype(DO_S)::value, do_p = decltype(DO_P)::value;
-    // check: stash only tiles below ntiles; void: the prologue, nothing to stash
-    constexpr bool check = kStashCheck<decltype(CHECK)>;
-    constexpr bool do_g = !std::is_same_v<decltype(CHECK), std::nullptr_t>;
-    f32x16(&sp)[2] = sc[np];
-    if constexpr (do_p) {
-      const int n0 = tp * kTileKV;
-      // Lane holds tokens n0 + 32 mt + 8 (v / 4) + 4 h + v % 4 of its row.
-      if (n0 + kTileKV - 1 > first_pos || n0 + kTileKV > kvl) {   // uniform
-        const int lim = min(qpos + 1, kvl);
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int v = 0; v < 16; ++v)
-            if (n0 + 32 * mt + 8 * (v >> 2) + 4 * h + (v & 3) >= lim) sp[mt][v] = -INFINITY;
-      }
-      if (any_bad) {   // uniform; the 4 tokens of a group share one page (page_size >= 4)
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int v4 = 0; v4 < 4; ++v4)
-            if (uint32_t(page_of(n0 + 32 * mt + 8 * v4 + 4 * h)) >= uint32_t(a.num_pages))
-#pragma unroll
-              for (int e = 0; e < 4; ++e) sp[mt][4 * v4 + e] = -INFINITY;
-      }
-    }
-    const T* kt = sK + (ts & 1) * kKHalves + kb0;
-    V8 ka[kAhead + 1];
-    if constexpr (do_s) {
-#pragma unroll
-      for (int i = 0; i < kAhead; ++i) ka[i] = k_op(kt, i);
-    }
-    float mx = -INFINITY;
-    KSV_ORDER();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (do_s) {
-        ka[(i + kAhead) % (kAhead + 1)] = k_op(kt, i + kAhead);
-        sc[ns][i & 1] = mfma32(ka[i % (kAhead + 1)], qf[i >> 1], i < 2 ? f32x16{} : sc[ns][i & 1]);
-      }
-      if constexpr (do_p) {
-#pragma unroll
-        for (int e = 8 * i; e < 8 * i + 8; ++e) mx = fmaxf(mx, sp[e >> 4][e & 15]);
-      }
-      KSV_ORDER();
-    }
-    if constexpr (do_p) {
-      // max with the other half of the row (lane ^ 32), by a lane swap
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
-                                                       false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * a.scale_log2;
-      // Lazy running max (see paged_prefill_kernel).
-      if (__any(mx > m + 8.f)) {
-        const float m_new = mx > m + 8.f ? mx : m;
-        const float alpha = fast_exp2(m - m_new);
-        m = m_new;
-        lsum *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-      }
-    }
-    KSV_ORDER();
-#pragma unroll
-    for (int i = 4; i < 16; ++i) {
-      if constexpr (do_s) {
-        if (i + kAhead < 16) ka[(i + kAhead) % (kAhead + 1)] = k_op(kt, i + kAhead);
-        sc[ns][i & 1] = mfma32(ka[i % (kAhead + 1)], qf[i >> 1], sc[ns][i & 1]);
-      }
-      if (do_g && i >= 4 && i < 4 + 2 * kW4Loads && (i & 1) == 0) {
-        const int l = (i - 4) >> 1;
-        if (!check || tg + 2 < ntiles) put_k(tg + 2, gk[G][l], l);
-        if (!check || tg + 1 < ntiles) put_vt(tg + 1, gv[G], l, gv_ok[G]);
-      }
-      if constexpr (do_p) {
-        // probability pairs pp = 4 (i - 4) / 3 .. : 16 pairs over 12 MFMAs
-#pragma unroll
-        for (int pp = 0; pp < 16; ++pp) {
-          if (4 + 3 * pp / 4 != i) continue;
-          const int mt = pp >> 3, v = (2 * pp) & 15, k = 2 * mt + (v >> 3), w = (v & 7) >> 1;
-          pb[k][2 * w] = T(fast_exp2(fmaf(sp[mt][v], a.scale_log2, -m)));
-          pb[k][2 * w + 1] = T(fast_exp2(fmaf(sp[mt][v + 1], a.scale_log2, -m)));
-          // An empty asm reading the packed pair keeps the compiler from
-          // sinking the exponentials to their MFMA in phase B.
-          const uint32_t word = __builtin_bit_cast(u32x4, pb[k])[w];
-          asm volatile("" ::"v"(word));
-        }
-      }
-      KSV_ORDER();
-    }
-  };
-  // Phase B: O += V(tp)^T . P^T (do_p) with the row sum between the MFMAs,
-  // then (do_g) stash gather unit G (K(tg + 2), V(tg + 1)) and issue the
-  // loads of the unit two iterations on.
-  auto phase_b = [&](int tp, auto DO_P, int G, int tg) __attribute__((always_inline)) {
-    constexpr bool do_p = decltype(DO_P)::value;
-    const T* vt = sVt + (tp & 1) * kVtHalves + vb0;
-    V8 va[kAhead + 1];
-    if constexpr (do_p) {
-#pragma unroll
-      for (int i = 0; i < kAhead; ++i) va[i] = v_op(vt, i);
-    }
-    float ps = 0.f;
-    KSV_ORDER();
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if constexpr (do_p) {
-        if (i + kAhead < 16) va[(i + kAhead) % (kAhead + 1)] = v_op(vt, i + kAhead);
-        o[i & 3] = mfma32(va[i % (kAhead + 1)], pb[i >> 2], o[i & 3]);
-        if ((i & 3) == 0) ps = dot8(pb[i >> 2], ones, ps);
-      }
-      if (i < kW4Loads) {
-        gk[G][i] = load_tok(kbase, atk, i);
-        gv[G][i] = load_tok(vbase, atv, i);
-        if (i == 0) gv_ok[G] = atv.nok;
-      } else if (i == kW4Loads) {
-        // next iteration: K of tile tg + 5, V of tile tg + 4
-        atv = atk;
-        atk = at_tile(tg + 5);
-      }
-      KSV_ORDER();
-    }
-    if constexpr (do_p) lsum += ps;
-  };
-
-  // Prologue: K(j_lo), V(j_lo) and K(j_lo + 1) into LDS and gather units
-  // j_lo and j_lo + 1 in flight, all loads issued together; S of tile j_lo.
-  {
-    const TileAt i0 = at_tile(j_lo), i1 = at_tile(j_lo + 1), i2 = at_tile(j_lo + 2),
-                 i3 = at_tile(j_lo + 3);
-    V8 k0[kW4Loads], v0[kW4Loads], k1[kW4Loads];
-    // Unit 1 is issued after all of unit 0: the loop's first stash waits
-    // for unit 0 only, with the same count on entry as from the back edge.
-#pragma unroll
-    for (int i = 0; i < kW4Loads; ++i) {
-      k0[i] = load_tok(kbase, i0, i);
-      v0[i] = load_tok(vbase, i0, i);
-      k1[i] = load_tok(kbase, i1, i);
-      gk[0][i] = load_tok(kbase, i2, i);
-      gv[0][i] = load_tok(vbase, i1, i);
-    }
-#pragma unroll
-    for (int i = 0; i < kW4Loads; ++i) {
-      gk[1][i] = load_tok(kbase, i3, i);
-      gv[1][i] = load_tok(vbase, i2, i);
-    }
-    gv_ok[0] = i1.nok;
-    gv_ok[1] = i2.nok;
-    atk = at_tile(j_lo + 4);
-    atv = i3;
-#pragma unroll
-    for (int i = 0; i < kW4Loads; ++i) {
-      put_k(j_lo, k0[i], i);
-      put_vt(j_lo, v0, i, i0.nok);
-      put_k(j_lo + 1, k1[i], i);
-    }
-  }
-  __syncthreads();
-  constexpr std::true_type yes{};
-  constexpr std::false_type no{};
-  if (j_last >= j_lo) phase_a(0, j_lo, yes, 1, j_lo, no, 0, j_lo, nullptr);
-  __syncthreads();   // iteration j_lo overwrites K(j_lo), read just above
-
-  // Iteration t: phase A computes S(t + 1) into sc[n] and the softmax of
-  // sc[1 - n] (n = 1 for even t - j_lo); unrolled by two so that every
-  // register array index is a constant. While this wave needs both halves
-  // of both phases (t + 1 <= j_last) the iterations are straight-line code;
-  // the last few pick the variant of each phase they need.
-  constexpr std::integral_constant<int, 0> zero{};
-  constexpr std::integral_constant<int, 1> one{};
-  auto steady = [&](int t, auto N) __attribute__((always_inline)) {
-    constexpr int n = decltype(N)::value;
-    phase_a(n, t + 1, yes, 1 - n, t, yes, 1 - n, t, no);
-    phase_b(t, yes, 1 - n, t);
-    __syncthreads();
-  };
-  auto tail = [&](int t, auto N) __attribute__((always_inline)) {
-    constexpr int n = decltype(N)::value;
-    if (t + 1 <= j_last)
-      phase_a(n, t + 1, yes, 1 - n, t, yes, 1 - n, t, yes);
-    else if (t <= j_last)
-      phase_a(n, t + 1, no, 1 - n, t, yes, 1 - n, t, yes);
-    else
-      phase_a(n, t + 1, no, 1 - n, t, no, 1 - n, t, yes);
-    if (t <= j_last)
-      phase_b(t, yes, 1 - n, t);
-    else
-      phase_b(t, no, 1 - n, t);
-    __syncthreads();
-  };
-  int t = j_lo;
-  for (; t + 2 <= j_last; t += 2) {
-    steady(t, one);
-    steady(t + 1, zero);
-  }
-  for (; t < ntiles; t += 2) {
-    tail(t, one);
-    if (t + 1 >= ntiles) break;
-    tail(t + 1, zero);
-  }
-
-  lsum += __shfl_xor(lsum, 32);
-  if (!row_ok) return;
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  if (slot < 0) {
-    f16* op = a.out + int64_t(qb + qrow) * a.o_tok + int64_t(hq) * a.o_head;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const V4 val = {T(o[dt][4 * g] * inv), T(o[dt][4 * g + 1] * inv),
-                        T(o[dt][4 * g + 2] * inv), T(o[dt][4 * g + 3] * inv)};
-        *reinterpret_cast<V4*>(op + 32 * dt + 8 * g + 4 * h) = val;
-      }
-    return;
-  }
-  const int64_t prow = int64_t(slot) * kTileQ + (qrow - q0);
-  float* po = a.part_o + prow * kD;
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 val = {o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
-                         o[dt][4 * g + 3] * inv};
-      *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * g + 4 * h) = val;
-    }
-  if (h == 0) {
-    a.part_ml[2 * prow] = m;
-    a.part_ml[2 * prow + 1] = lsum;
-  }
-}
-#undef KSV_ORDER
 
 // Combines the splits of one (sequence, q tile, q head): weight of split j
 // = 2^(m_j - max m) * sum_j, taken in split order.
@@ -1059,12 +672,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_append_kernel(RopeArgs a) {
 template <typename T>
 int run_prefill(const PrefillArgs& a, const MergeArgs& m, int num_tiles, int num_merge,
                 bool staged, hipStream_t s) {
-  if constexpr (kPrefillOneWavePerSimd) {
-    if (staged)
-      paged_prefill_w4_kernel<T, true><<<dim3(num_tiles), kW4Threads, 0, s>>>(a);
-    else
-      paged_prefill_w4_kernel<T, false><<<dim3(num_tiles), kW4Threads, 0, s>>>(a);
-  } else if (staged) {
+  if (staged) {
     paged_prefill_kernel<T, true><<<dim3(num_tiles), kThreads, 0, s>>>(a);
   } else {
     paged_prefill_kernel<T, false><<<dim3(num_tiles), kThreads, 0, s>>>(a);
