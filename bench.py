@@ -269,7 +269,7 @@ def copy_ceiling(pool, r, reps, device):
     first 8192 blocks of K and V into the next 8192 (16 GiB read + 16 GiB
     written, as the remap copy). kunserve_hbm_probe has the block copy's
     launch shape; the memcpy goes through torch's copy_ of contiguous
-    same-device tensors, which is one hipMemcpyAsync. Leaves the pool's
+    same-device tensors, which is one hipMemcpyAsync. Leaves the
     pool's bytes overwritten: run it before the pool is filled."""
     from kunserve_amd import _lib
 
