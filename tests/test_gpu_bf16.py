@@ -1,7 +1,8 @@
 """bf16 pools (the reference's default --dtype, kunserve/kunserve_config.py:61)
 on the GPU vs the CPU oracle evaluated on the same bf16 values.
 
-Attention: max-abs <= ATOL_BF16 (bf16 keeps 8 significant bits to fp16's 11).
+Attention: max-abs <= ATOL_BF16 (bf16 keeps 8 significant bits to fp16's 11)
+and relative Frobenius error <= RTOL_BF16.
 RoPE: one bf16 ulp plus 1e-6. Block movement: bit-exact (byte copies)."""
 import math
 
@@ -14,8 +15,8 @@ from kunserve_amd import (AttentionStep, DecodePlan, LlamaOp, PrefillPlan, appen
                           rope_inv_freq)
 from oracle import paged_attention_ref as ref
 
-from helpers import (ATOL_BF16, compact_for_oracle, max_abs, random_pool, random_tensor,
-                     table_from_csr, to_numpy)
+from helpers import (ATOL_BF16, RTOL_BF16, compact_for_oracle, max_abs, random_pool,
+                     random_tensor, rel_err, table_from_csr, to_numpy)
 
 pytestmark = pytest.mark.gpu
 BF16 = torch.bfloat16
@@ -44,6 +45,7 @@ def test_bf16_decode_matches_oracle(device, head_dim, hq, hkv):
     k, v, ip, ix = compact_for_oracle(pool, 0, indptr, indices)
     want = ref.decode_attention(to_numpy(q), k, v, 0, ip, ix, kv, 1 / math.sqrt(head_dim))
     assert max_abs(out, want) <= ATOL_BF16
+    assert rel_err(out, want) <= RTOL_BF16, rel_err(out, want)
 
 
 @pytest.mark.parametrize("num_cus", [1, 1024])
@@ -64,6 +66,7 @@ def test_bf16_prefill_matches_oracle(device, num_cus):
     k, v, ip, ix = compact_for_oracle(pool, 0, indptr, indices)
     want = ref.prefill_attention(to_numpy(q), q_indptr, k, v, 0, ip, ix, kv, 1 / math.sqrt(128))
     assert max_abs(out, want) <= ATOL_BF16
+    assert rel_err(out, want) <= RTOL_BF16, rel_err(out, want)
 
 
 def test_bf16_rope_append_and_block_moves(device):
@@ -124,6 +127,7 @@ def test_bf16_llama_op_mixed_step(device):
     want = ref.prefill_attention(to_numpy(q), q_indptr, k_pool0, v_pool0, 1, indptr, indices, kv,
                                  1 / math.sqrt(128))
     assert out.dtype == BF16 and max_abs(out, want) <= ATOL_BF16
+    assert rel_err(out, want) <= RTOL_BF16, rel_err(out, want)
 
 
 def test_bf16_decode_on_256_token_pages(device):
@@ -144,3 +148,4 @@ def test_bf16_decode_on_256_token_pages(device):
     k, v, ip, ix = compact_for_oracle(pool, 0, indptr, indices, np.arange(len(kv)))
     want = ref.decode_attention(to_numpy(q), k, v, 0, ip, ix, kv, 1.0 / math.sqrt(128))
     assert max_abs(out, want) <= ATOL_BF16
+    assert rel_err(out, want) <= RTOL_BF16, rel_err(out, want)

@@ -9,7 +9,7 @@ from kunserve_amd import DecodePlan, paged_decode, workloads
 from oracle import paged_attention_ref as ref
 
 from helpers import (ATOL, ATOL_BF16, compact_for_oracle, max_abs, random_pool, random_tensor,
-                     table_from_csr, to_numpy)
+                     table_from_csr, to_numpy, torch_decode_ref)
 
 pytestmark = pytest.mark.gpu
 
@@ -129,10 +129,12 @@ def test_decode_page_permutation_bit_exact(device):
     assert torch.equal(out, out2)
 
 
-def test_llama2_7b_decode_all_layers_sampled(device):
-    """Full Llama-2-7B decode shape (32 layers, 16384-page pool, batch 64);
-    every layer is checked on a sample of rows, always including the
-    longest and the shortest."""
+def test_llama2_7b_decode_every_layer_and_row(device):
+    """Full Llama-2-7B decode shape (32 layers, 16384-page pool, batch 64):
+    every row of every layer against the fp32 reference on the device, and
+    a sample of rows of three layers (the longest and the shortest among
+    them) against the numpy oracle as well, which pins that reference at
+    this shape."""
     w = workloads.llama2_7b_decode()
     pool = random_pool(w.num_pages, w.num_layers, w.num_kv_heads, w.page_size, w.head_dim,
                        device, 71)
@@ -141,19 +143,27 @@ def test_llama2_7b_decode_all_layers_sampled(device):
     plan = DecodePlan(w.kv_len, w.num_qo_heads, w.num_kv_heads, device)
     order = np.argsort(w.kv_len)
     rows = np.unique(np.concatenate([order[:2], order[-2:], order[::16]]))
-    for layer in (0, 13, 31):
+    for layer in range(w.num_layers):
         q = random_tensor((w.batch, w.num_qo_heads, w.head_dim), device, 100 + layer)
         out = paged_decode(pool, layer, table, q, plan)
-        want = oracle_decode(pool, layer, indptr, indices, w.kv_len, q, rows)
-        assert max_abs(out[torch.from_numpy(rows).to(device)], want) <= ATOL
+        full = torch_decode_ref(pool, layer, indptr, indices, w.kv_len, q)
+        assert max_abs(out, full) <= ATOL, f"layer {layer}"
+        if layer in (0, 13, 31):
+            want = oracle_decode(pool, layer, indptr, indices, w.kv_len, q, rows)
+            assert max_abs(out[torch.from_numpy(rows).to(device)], want) <= ATOL
+            assert max_abs(full[torch.from_numpy(rows).to(device)], want) <= 1e-5
 
 
-def test_llama3_8b_gqa_decode_sampled(device):
+def test_llama3_8b_gqa_decode_every_row(device):
+    """Llama-3-8B GQA decode (32 q / 8 KV heads, batch 128, contexts
+    1024-8192, MFMA kernel with merges): every row against the fp32
+    reference on the device, sampled rows against the numpy oracle."""
     w = workloads.llama3_8b_gqa_decode()
     pool = random_pool(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device, 81)
     indptr, indices = w.csr()
     q, out, plan = run_decode(pool, 0, indptr, indices, w.kv_len, w.num_qo_heads, device, 82)
     assert plan.info.num_merge > 0 and plan.info.group_size == 4
+    assert max_abs(out, torch_decode_ref(pool, 0, indptr, indices, w.kv_len, q)) <= ATOL
     order = np.argsort(w.kv_len)
     rows = np.unique(np.concatenate([order[:2], order[-3:], order[::32]]))
     want = oracle_decode(pool, 0, indptr, indices, w.kv_len, q, rows)
@@ -164,8 +174,8 @@ def test_llama2_70b_decode_on_remapped_tables(device):
     """Block remap under memory pressure: copy 8192 random blocks between
     disjoint regions, then decode a Llama-2-70B layer (64 Q / 8 KV heads,
     batch 256, contexts U[256, 4096]) on tables pointing at the copies. The
-    result equals the decode on the original tables bit for bit, and the
-    oracle on sampled rows."""
+    result equals the decode on the original tables bit for bit, the fp32
+    reference on every row, and the oracle on sampled rows."""
     from kunserve_amd import copy_blocks
 
     r = workloads.kv_remap()
@@ -179,6 +189,7 @@ def test_llama2_70b_decode_on_remapped_tables(device):
     ip, ix = w.csr()
     _, out, _ = run_decode(pool, 5, ip, ix, w.kv_len, w.num_qo_heads, device, 92)
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    assert max_abs(out2, torch_decode_ref(pool, 5, ip2, ix2, w2.kv_len, q)) <= ATOL
     order = np.argsort(w.kv_len)
     rows = np.unique(np.concatenate([order[:2], order[-2:], order[::64]]))
     want = oracle_decode(pool, 5, ip2, ix2, w2.kv_len, q, rows)
