@@ -3,9 +3,13 @@
 Importing the package registers torch.ops.swapping_ops.swap with the
 reference schema (kunserve/worker.py:673-681), backed by the HIP library, so
 the reference's ParaWorker.swap_blocks call runs unchanged. LlamaOp mirrors
-the KV-cache side of torch.classes.gpt_ops.LlamaOp (kunserve/models.py:52-65).
+the KV-cache side of torch.classes.gpt_ops.LlamaOp (kunserve/models.py:52-65),
+and importing the package also makes that name resolve to it, so the
+reference's constructor call (12 ints) runs unchanged.
 """
 from __future__ import annotations
+
+import types
 
 import torch
 
@@ -48,3 +52,34 @@ try:
 except RuntimeError:
     # Already defined by another loader in this process.
     pass
+
+
+class _GptOpsNamespace(types.ModuleType):
+    """torch.classes.gpt_ops with LlamaOp bound to this package's class;
+    every other name is looked up among the natively registered classes."""
+
+    def __init__(self, native):
+        super().__init__("torch.classes.gpt_ops")
+        self._native = native
+        self.LlamaOp = LlamaOp
+
+    def __getattr__(self, name):
+        return getattr(self._native, name)
+
+
+def _register_gpt_ops() -> None:
+    """torch.classes resolves `torch.classes.<ns>.<Class>` through the C++
+    custom-class registry and caches the namespace object on torch.classes.
+    When no native gpt_ops.LlamaOp is registered, the cached namespace is
+    replaced by one whose LlamaOp is this package's class (a native one, if
+    a library registered it, is left in place)."""
+    native = torch.classes.gpt_ops
+    try:
+        native.LlamaOp
+        return
+    except RuntimeError:
+        pass
+    setattr(torch.classes, "gpt_ops", _GptOpsNamespace(native))
+
+
+_register_gpt_ops()

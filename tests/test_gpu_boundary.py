@@ -169,6 +169,32 @@ def test_pforward_with_tensor_cores(device):
     assert max_abs(out, want) <= ATOL
 
 
+def test_reference_constructor_call(device):
+    """The reference's own constructor call (kunserve/models.py:52-65: 12
+    positional ints, Llama-2-7B values at a small page count) through
+    torch.classes.gpt_ops.LlamaOp, then a decode step of pforward's 13
+    arguments (kunserve/worker.py:298-312) against the oracle."""
+    op = torch.classes.gpt_ops.LlamaOp(64, 2, 32, 32, 16, 128, 11008, 32000, 8, 4096, 4096, 1)
+    assert isinstance(op, LlamaOp) and op.pool.k.device == device
+    op.pool.k.copy_(random_tensor(op.pool.k.shape, device, 31))
+    op.pool.v.copy_(random_tensor(op.pool.v.shape, device, 32))
+    first, flags, q_lens = [37, 100], [0, 0], [1, 1]
+    pages = [[3, 9, 4], [10, 11, 12, 13, 14, 15, 16]]
+    step = op.pforward(2, 2, 64, 0, 2, [[0], [0]], first, flags, pages)
+    q = random_tensor((2, 32, 128), device, 33)
+    k = random_tensor((2, 32, 128), device, 34)
+    v = random_tensor((2, 32, 128), device, 35)
+    kh, vh = to_numpy(op.pool.k), to_numpy(op.pool.v)
+    out = step.run(1, q, k, v)
+    torch.cuda.synchronize()
+    kv = ref.kv_lens_for_step(first, q_lens, flags)
+    q_indptr = np.array([0, 1, 2])
+    indptr, indices = csr(pages)
+    ref.append_kv(kh, vh, 1, indptr, indices, kv, q_indptr, to_numpy(k), to_numpy(v))
+    want = ref.decode_attention(to_numpy(q), kh, vh, 1, indptr, indices, kv, 1 / math.sqrt(128))
+    assert max_abs(out, want) <= ATOL
+
+
 def test_shim_never_waits_for_the_device(device):
     """A mixed pforward step, its per-layer run, a local block copy and a
     kv_exchange pack, all with torch's sync debug mode set to raise."""

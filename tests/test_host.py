@@ -125,3 +125,17 @@ def test_pmm_pool_needs_a_gpu_device():
 
     with pytest.raises(ValueError, match="GPU device"):
         PmmPool(8, 2, 2, 16, 128, 8, device=torch.device("cpu"))
+
+
+def test_reference_class_names_resolve_to_this_package():
+    """kunserve/models.py:52-65 constructs torch.classes.gpt_ops.LlamaOp and
+    kunserve/worker.py:673-681 calls torch.ops.swapping_ops.swap: both names
+    resolve to this package once it is imported."""
+    import torch
+
+    import kunserve_amd
+
+    assert torch.classes.gpt_ops.LlamaOp is kunserve_amd.LlamaOp
+    assert hasattr(torch.ops.swapping_ops, "swap")
+    with pytest.raises(RuntimeError):   # other gpt_ops names stay native lookups
+        torch.classes.gpt_ops.NotAClassOfThisPackage
