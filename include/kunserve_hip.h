@@ -267,14 +267,18 @@ typedef struct {
   int32_t num_merge;     /* (tile, head) items whose KV range is split     */
   int32_t num_slots;     /* partial-result slots of the split items        */
   int32_t kv_chunk;      /* split length in tokens (0: nothing split)      */
+  int32_t head_dim;      /* head_dim the plan was made for                 */
 } kunserve_prefill_plan_info;
 
-/* Upper bound of the prefill plan length (int32 entries). */
+/* Upper bound of the prefill plan length (int32 entries); -1 for a bad
+ * argument or a head_dim other than 64, 128 and 256. */
 int64_t kunserve_prefill_plan_bound(const int32_t* q_indptr_host,
-                                    int32_t num_seqs, int32_t num_qo_heads);
+                                    int32_t num_seqs, int32_t num_qo_heads,
+                                    int32_t head_dim);
 
 /* Host-side plan: tiles the ragged q rows (q_len[b] = q_indptr[b+1] -
- * q_indptr[b]) of every q head into tiles of tile_q rows, and orders the
+ * q_indptr[b]) of every q head into tiles of tile_q rows (256 for head_dim
+ * 64 and 128, 128 for 256; other head dims: KUNSERVE_EUNSUPPORTED), and orders the
  * (row, tile, head) items so that items reading the same K/V (same row and
  * KV head) run back to back on one XCD (one L2), longest first. When the
  * items cannot fill num_cus CUs twice over (0: 256 CUs), each item's KV
@@ -286,7 +290,7 @@ int64_t kunserve_prefill_plan_bound(const int32_t* q_indptr_host,
 int kunserve_prefill_plan(const int32_t* q_indptr_host,
                           const int32_t* kv_len_host, int32_t num_seqs,
                           int32_t num_qo_heads, int32_t num_kv_heads,
-                          int32_t num_cus, int32_t* plan_host,
+                          int32_t head_dim, int32_t num_cus, int32_t* plan_host,
                           int64_t plan_capacity,
                           kunserve_prefill_plan_info* info);
 
@@ -299,7 +303,8 @@ int64_t kunserve_prefill_workspace_bytes(const kunserve_prefill_plan_info* info)
  * sequence b sees positions [0, kv_len[b] - q_len[b] + i]. q and out are
  * [num_tokens, num_qo_heads, head_dim] of the pool dtype with rows grouped
  * by q_indptr. fp16 or bf16 MFMA for Q.K^T and P.V, fp32 accumulation and
- * softmax. */
+ * softmax. head_dim 64, 128 or 256 (KUNSERVE_EUNSUPPORTED otherwise); the
+ * plan must have been made for the pool's head_dim. */
 int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
                            const kunserve_page_table* table,
                            const int32_t* q_indptr_dev,

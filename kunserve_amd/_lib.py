@@ -57,7 +57,7 @@ class DecodePlanInfo(Structure):
 class PrefillPlanInfo(Structure):
     _fields_ = [("num_tiles", c_int32), ("tile_q", c_int32), ("plan_ints", c_int32),
                 ("num_qo_heads", c_int32), ("max_kv_len", c_int32), ("num_merge", c_int32),
-                ("num_slots", c_int32), ("kv_chunk", c_int32)]
+                ("num_slots", c_int32), ("kv_chunk", c_int32), ("head_dim", c_int32)]
 
 
 # name -> (restype, argtypes); must match include/kunserve_hip.h.
@@ -91,9 +91,9 @@ SIGNATURES = {
                                               POINTER(Tensor3), POINTER(Tensor3), c_int32,
                                               c_float, c_void_p, POINTER(DecodePlanInfo),
                                               c_void_p]),
-    "kunserve_prefill_plan_bound": (c_int64, [c_void_p, c_int32, c_int32]),
+    "kunserve_prefill_plan_bound": (c_int64, [c_void_p, c_int32, c_int32, c_int32]),
     "kunserve_prefill_plan": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
-                                      c_void_p, c_int64, POINTER(PrefillPlanInfo)]),
+                                      c_int32, c_void_p, c_int64, POINTER(PrefillPlanInfo)]),
     "kunserve_prefill_workspace_bytes": (c_int64, [POINTER(PrefillPlanInfo)]),
     "kunserve_paged_prefill": (c_int, [POINTER(KVPool), c_int32, POINTER(PageTable), c_void_p,
                                        POINTER(Tensor3), POINTER(Tensor3), c_int32, c_float,

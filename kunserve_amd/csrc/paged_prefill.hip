@@ -33,16 +33,39 @@
 namespace kunserve {
 namespace {
 
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kTileQ = 32 * kWaves;   // query rows per workgroup
 constexpr int kTileKV = 64;           // kv tokens per iteration
-constexpr int kD = 128;               // head_dim of the MFMA kernel
+constexpr int kVtPitch = kTileKV;     // halves per row of the transposed V tile
 constexpr int kXcds = 8;              // MI355X: workgroup i runs on XCD i % 8
-// A gathering thread moves 4 consecutive tokens; 4 waves of 16 tokens make
-// one tile.
-static_assert(kTileKV == 4 * 16 && kThreads == 2 * 4 * kWave,
-              "half of the 8 waves gather K, the other half V");
+
+// Geometry of the attention kernel for one head_dim. Every wave owns 32
+// query rows (the 32x32 MFMA's columns). Up to head_dim 128 a workgroup is
+// 8 waves, two per SIMD; at 256 it is 4 waves, one per SIMD, since the O
+// accumulators and Q operands of a wave then take 192 registers.
+template <int D>
+struct Geom {
+  static_assert(D == 64 || D == 128 || D == 256, "prefill head_dim is 64, 128 or 256");
+  static constexpr int kWaves = D <= 128 ? 8 : 4;
+  static constexpr int kThreads = kWaves * kWave;
+  static constexpr int kTileQ = 32 * kWaves;   // query rows per workgroup
+  static constexpr int kSteps = D / 16;        // 16-dim k-steps of S = K.Q^T
+  static constexpr int kBlocks = D / 32;       // 32-dim blocks of O
+  static constexpr int kKPitch = D + 8;        // halves per K row
+  static constexpr int kKHalves = kTileKV * kKPitch;
+  static constexpr int kVtHalves = D * kVtPitch;
+  // Gather units (4 consecutive tokens x one 16-byte chunk of K or V) per
+  // lane of a gathering wave: 64 and 128: one (waves 0-1 / 0-3 gather V,
+  // 2-3 / 4-7 gather K); 256: four (every wave two chunks of V and two of K).
+  static constexpr int kUnits = D == 256 ? 4 : 1;
+  // Gather register sets: two (the tile after next in flight while the next
+  // waits to be stashed) up to 128; one at 256, whose register file holds
+  // no second set, and whose tiles take twice the math to cover the loads.
+  static constexpr int kRegSets = D <= 128 ? 2 : 1;
+};
+
+constexpr int tile_q_for(int head_dim) { return head_dim <= 128 ? 256 : 128; }
+static_assert(tile_q_for(64) == Geom<64>::kTileQ && tile_q_for(128) == Geom<128>::kTileQ &&
+                  tile_q_for(256) == Geom<256>::kTileQ,
+              "the plan's tile is the kernel's");
 
 struct PrefillArgs {
   const f16* q;
@@ -60,8 +83,8 @@ struct PrefillArgs {
   const int32_t* kv_len;
   const int32_t* q_indptr;
   const int32_t* tiles;   // [num_tiles][kRec]: see kRec
-  float* part_o;          // [slots][kTileQ][kD] split partials, normalised
-  float* part_ml;         // [slots][kTileQ][2] running max (log2 units), sum
+  float* part_o;          // [slots][tile_q][head_dim] split partials, normalised
+  float* part_ml;         // [slots][tile_q][2] running max (log2 units), sum
   int32_t ratio;
   float scale_log2;
 };
@@ -77,9 +100,9 @@ constexpr int kMergeRec = 5;
 // 8-byte stores go 16 lanes per cycle over 32 banks; the 16-byte accesses
 // below measured conflict-free (16-byte reads follow no simple lane-group
 // model, so layouts were chosen by measurement).
-// K tile: row-major [token][dim], rows 68 dwords apart; operand reads (row
-//   32 mt + r, one 16-byte chunk) and the gather's 16-byte row stores are
-//   conflict-free.
+// K tile: row-major [token][dim], rows head_dim + 8 halves apart (68
+//   dwords at 128); operand reads (row 32 mt + r, one 16-byte chunk) and the
+//   gather's 16-byte row stores are conflict-free.
 // V tile: transposed, row d holds dim d of the tile's 64 tokens, rows 128
 //   bytes apart, so the V^T operands are plain 16-byte reads (the gfx950
 //   transposing read, ds_read_b64_tr_b16, moves a quarter of the bytes per
@@ -89,36 +112,38 @@ constexpr int kMergeRec = 5;
 //   chunk. Chunk c of row d is stored at chunk c ^ ((d ^ (d >> 3)) & 7):
 //   conflict-free for both the operand reads and the gather's 8-byte stores
 //   (a store pass, 16 lanes, covers 8 dims 8 apart x both halves of a chunk).
-constexpr int kKPitch = kD + 8;     // halves
-constexpr int kKHalves = kTileKV * kKPitch;
-constexpr int kVtPitch = kTileKV;   // halves
-constexpr int kVtHalves = kD * kVtPitch;
-
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Gather layout: lane l of a gathering wave with token group g (0..3) moves
-// dims 8 c .. +8, c = (l & 7) | ((l >> 4) & 1) << 3, of the 4 consecutive
-// tokens gather_token(g, l) + i, i < 4; a load round reads 4 whole 256-byte
-// rows per wave (lanes 8 apart cover a row's halves). The tokens are
-// 4-aligned, so (page_size >= 4) one page holds them.
-__device__ __forceinline__ int gather_token(int g, int lane) {
-  return 16 * g + 8 * ((lane >> 3) & 1) + 4 * (lane >> 5);
+// Gather layout. A lane moves 4 consecutive tokens 16 g + 8 a + 4 h + i
+// (i < 4) of 16-byte chunks c of K or V: token group g (0..3), a and h pick
+// the lane's 4 tokens within the group. Lane bits: c = l & 7 and a = bit 3
+// always, so that every 16 lanes cover both halves a of 8 chunks (the
+// transposed stores' conflict-free pass); then, at head_dim 64, h = bit 4
+// and g = 2 w + bit 5 (wave w of a pair); at 128 and 256, c |= bit 4 << 3,
+// h = bit 5 and g = the wave's group (256: chunks 16..31 as a second
+// unit). The tokens are 4-aligned, so (page_size >= 4) one page holds them.
+struct GatherLane {
+  int g, c, a, h;
+};
+template <int D>
+__device__ __forceinline__ GatherLane gather_lane(int group, int lane) {
+  if constexpr (D == 64)
+    return {2 * group + (lane >> 5), lane & 7, (lane >> 3) & 1, (lane >> 4) & 1};
+  else
+    return {group, (lane & 7) | (((lane >> 4) & 1) << 3), (lane >> 3) & 1, lane >> 5};
 }
-__device__ __forceinline__ int gather_chunk(int lane) { return (lane & 7) | (((lane >> 4) & 1) << 3); }
-__device__ __forceinline__ int gather_dim(int lane) { return 8 * gather_chunk(lane); }
 
-// Transposed store of dims 2 part, 2 part + 1 of a gathering lane's 4
-// tokens (x[i]: token i, 8 dims) into the V^T buffer buf. Dim 8 c + e of
-// token group g is row 8 c + e, logical chunk 2 g + h, stored at chunk
-// (2 g + h) ^ c ^ e (c, e < 8 here), at half 4 a of it. v_perm builds each
+// Transposed store of dims 2 part, 2 part + 1 of chunk c of a gathering
+// lane's 4 tokens (x[i]: token i, 8 dims) into the V^T buffer buf. Dim
+// 8 c + e of token group g is row 8 c + e, logical chunk 2 g + h, stored at
+// chunk (2 g + h) ^ (c & 7) ^ e, at half 4 a of it. v_perm builds each
 // dword from two tokens' dwords; its selector byte 0x0c yields a zero
 // byte, which zeroes the tokens from nok on.
 template <typename T>
-__device__ __forceinline__ void vt_store(T* buf, int g, int lane,
+__device__ __forceinline__ void vt_store(T* buf, const GatherLane& gl, int c,
                                          const typename Vec<T>::v8 (&x)[4], int part, int nok) {
-  const int c = gather_chunk(lane), a = (lane >> 3) & 1, h = lane >> 5;
-  const int row0 = 8 * c * kVtPitch + 4 * a;
-  const int chunk0 = (2 * g + h) ^ (c & 7);
+  const int row0 = 8 * c * kVtPitch + 4 * gl.a;
+  const int chunk0 = (2 * gl.g + gl.h) ^ (c & 7);
   const uint32_t z01 = (nok < 1 ? 0x0000ffffu : 0u) | (nok < 2 ? 0xffff0000u : 0u);
   const uint32_t z23 = (nok < 3 ? 0x0000ffffu : 0u) | (nok < 4 ? 0xffff0000u : 0u);
 #pragma unroll
@@ -137,8 +162,9 @@ __device__ __forceinline__ void vt_store(T* buf, int g, int lane,
 
 // V^T operand (ks, dt) of lane (r, h): row d = 32 dt + r, logical chunk
 // 2 ks + h, stored at chunk (2 ks + h) ^ ((d ^ (d >> 3)) & 7)
-// = (2 ks ^ 4 (dt & 1)) ^ (h ^ (r & 7) ^ (r >> 3)): one of four per-lane
-// bases, j = ks ^ 2 (dt & 1), plus an immediate offset.
+// = (2 ks ^ 4 (dt & 1)) ^ (h ^ (r & 7) ^ (r >> 3)) (r >> 3 < 4, so d >> 3
+// adds no carry into bit 2): one of four per-lane bases, j = ks ^ 2 (dt & 1),
+// plus an immediate offset.
 struct VtBases {
   int b[4];
 };
@@ -179,14 +205,15 @@ constexpr int kMaxStagedPages = 2048;
 // issue only K/V loads; waiting for an older tile's data then leaves the
 // newer tile's loads in flight. Rows with more pages than fit use the
 // global-lookup variant (same results).
-template <typename T, bool STAGED>
-__global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) {
+template <typename T, int D, bool STAGED>
+__global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(PrefillArgs a) {
   typedef typename Vec<T>::v8 V8;
   typedef typename Vec<T>::v4 V4;
+  typedef Geom<D> G;
   __shared__ int s_pg[STAGED ? kMaxStagedPages : 1];
-  __shared__ int s_bad[kWaves];
-  __shared__ __attribute__((aligned(16))) T sK[2 * kKHalves];
-  __shared__ __attribute__((aligned(16))) T sVt[2 * kVtHalves];
+  __shared__ int s_bad[G::kWaves];
+  __shared__ __attribute__((aligned(16))) T sK[2 * G::kKHalves];
+  __shared__ __attribute__((aligned(16))) T sVt[2 * G::kVtHalves];
 
   const int32_t* item = a.tiles + kRec * blockIdx.x;
   const int seq = item[0];
@@ -217,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   const bool wave_active = q0 + wave * 32 < q_len;
   const int wave_first_pos = prefix + q0 + wave * 32;
   const int wave_last_pos = prefix + min(q0 + wave * 32 + 31, q_len - 1);
-  const int kv_end = min(prefix + min(q0 + kTileQ, q_len), kv_hi);   // exclusive
+  const int kv_end = min(prefix + min(q0 + G::kTileQ, q_len), kv_hi);   // exclusive
   const int ntiles = (kv_end + kTileKV - 1) / kTileKV;   // tiles [kv_lo / kTileKV, ntiles)
   const int pg_lo = kv_lo >> a.page_shift;   // first staged page
   // Stage (or, for rows with too many pages, only scan) the page ids of
@@ -228,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   {
     const int npg = kv_end > kv_lo ? ((kv_end - 1) >> a.page_shift) + 1 - pg_lo : 0;
     bool bad_id = false;
-    for (int i = threadIdx.x; i < npg; i += kThreads) {
+    for (int i = threadIdx.x; i < npg; i += G::kThreads) {
       const int p = pages[pg_lo + i];
       const bool ok = p >= 0 && p < a.num_pages;
       if constexpr (STAGED) s_pg[i] = ok ? p : -1;
@@ -239,7 +266,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     __syncthreads();
     int bad = 0;
 #pragma unroll
-    for (int wv = 0; wv < kWaves; ++wv) bad |= s_bad[wv];
+    for (int wv = 0; wv < G::kWaves; ++wv) bad |= s_bad[wv];
     any_bad = __builtin_amdgcn_readfirstlane(bad) != 0;   // the same in every lane
   }
   // Whether kv token `tok` (< kv_end) lies on an out-of-range page.
@@ -249,16 +276,16 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   };
 
   // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
-  V8 qf[8];
+  V8 qf[G::kSteps];
   {
     const f16* qp = a.q + int64_t(qb + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = row_ok ? load_v8<T>(qp + 16 * s + 8 * h) : V8{};
+    for (int s = 0; s < G::kSteps; ++s) qf[s] = row_ok ? load_v8<T>(qp + 16 * s + 8 * h) : V8{};
   }
 
-  f32x16 o[4];
+  f32x16 o[G::kBlocks];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+  for (int i = 0; i < G::kBlocks; ++i) o[i] = f32x16{};
   float m = -1.0e30f;   // running max of this row, in scaled (log2) units
   float lsum = 0.f;     // this lane's share of the row sum (other half: lane ^ 32)
 
@@ -268,15 +295,26 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   // Tile registers: two sets, so that the gather of tile n + 2 is in flight
   // while tile n is computed and tile n + 1 waits to be parked in LDS. One
   // tile's loads take about one HBM round trip, longer than a tile's math.
-  // Waves 0-3 gather V (stored transposed), waves 4-7 K, token group
-  // wave % 4 (gather_token). The tile position of a gather is looked up one
-  // iteration ahead (at), so no lookup latency sits in front of the loads.
-  const bool gather_v = wave < 4;
-  const int ld_c = gather_dim(lane);
-  const int ld_t = gather_token(wave & 3, lane);
-  const f16* gbase = gather_v ? vbase : kbase;
+  // Gather roles (Geom::kUnits): at head_dim 64 waves 0-1 gather V and 2-3
+  // K; at 128 waves 0-3 V and 4-7 K; at 256 every wave both, two chunks of
+  // each. The tile position of a gather is looked up one iteration ahead
+  // (at), so no lookup latency sits in front of the loads. Every wave
+  // issues its loads unconditionally (at 64, waves 4-7 repeat those of
+  // waves 0-3, which the CU's cache serves, and do not stash them): a
+  // branch around loads makes the compiler wait for all loads in flight,
+  // the ones just issued too, wherever the branch joins.
+  constexpr int kGatherWaves = D == 64 ? 4 : G::kWaves;
+  const bool stashes = kGatherWaves == G::kWaves || wave < kGatherWaves;
+  const int gw = wave % kGatherWaves;
+  const bool gather_v = D == 256 || gw < kGatherWaves / 2;   // the first unit's tensor
+  const GatherLane gl = gather_lane<D>(D == 256 ? wave : gw % (kGatherWaves / 2), lane);
+  const int ld_t = 16 * gl.g + 8 * gl.a + 4 * gl.h;
+  const int ld_c = 8 * gl.c;
+  // Unit u: tensor (V for the first half at 256), chunk gl.c + 16 (u & 1) at 256.
+  auto unit_v = [&](int u) { return D == 256 ? u < 2 : gather_v; };
+  auto unit_c = [&](int u) { return gl.c + (D == 256 ? 16 * (u & 1) : 0); };
   struct Regs {
-    V8 x[4];
+    V8 x[G::kUnits][4];
     int nok;
   };
   TileAt at;
@@ -288,37 +326,46 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   };
   auto fetch = [&](Regs& rg) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rg.x[i] = load_v8<T>(gbase + at.off + int64_t(i) * a.token_stride);
+    for (int u = 0; u < G::kUnits; ++u) {
+      const f16* base = (unit_v(u) ? vbase : kbase) + at.off + 8 * (unit_c(u) - gl.c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rg.x[u][i] = load_v8<T>(base + int64_t(i) * a.token_stride);
+    }
     rg.nok = at.nok;
   };
   auto stash = [&](int buf, const Regs& rg) {
-    if (gather_v) {
+    if (!stashes) return;
 #pragma unroll
-      for (int part = 0; part < 4; ++part)
-        vt_store<T>(sVt + buf * kVtHalves, wave & 3, lane, rg.x, part, rg.nok);
-    } else {
+    for (int u = 0; u < G::kUnits; ++u) {
+      if (unit_v(u)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<V8*>(&sK[buf * kKHalves + (ld_t + i) * kKPitch + ld_c]) = rg.x[i];
+        for (int part = 0; part < 4; ++part)
+          vt_store<T>(sVt + buf * G::kVtHalves, gl, unit_c(u), rg.x[u], part, rg.nok);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<V8*>(&sK[buf * G::kKHalves + (ld_t + i) * G::kKPitch + 8 * unit_c(u)]) =
+              rg.x[u][i];
+      }
     }
   };
 
   // Per-lane LDS bases; each operand read adds a compile-time offset.
   // K A operand (S^T = K.Q^T): row 32 mt + r, dims 16 s + 8 h .. +8.
-  const int kb0 = r * kKPitch + 8 * h;
+  const int kb0 = r * G::kKPitch + 8 * h;
   const VtBases vb = vt_operand_bases(lane);
 
   auto compute = [&](int buf, int n0) {
-    const T* kt = sK + buf * kKHalves + kb0;
-    const T* vt = sVt + buf * kVtHalves;
+    const T* kt = sK + buf * G::kKHalves + kb0;
+    const T* vt = sVt + buf * G::kVtHalves;
     // S^T tiles: rows = kv tokens 32*mt + i, columns = query rows.
     f32x16 st[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      st[mt] = mfma32(*reinterpret_cast<const V8*>(kt + 32 * mt * kKPitch), qf[0], f32x16{});
+      st[mt] = mfma32(*reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch), qf[0], f32x16{});
 #pragma unroll
-      for (int s = 1; s < 8; ++s) {
-        const V8 ka = *reinterpret_cast<const V8*>(kt + 32 * mt * kKPitch + 16 * s);
+      for (int s = 1; s < G::kSteps; ++s) {
+        const V8 ka = *reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch + 16 * s);
         st[mt] = mfma32(ka, qf[s], st[mt]);
       }
     }
@@ -356,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
       m = m_new;
       lsum *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      for (int dt = 0; dt < G::kBlocks; ++dt) o[dt] *= alpha;
     }
 
     // P^T as B operands: k-step ks covers tokens 16ks + 4h + {0..3} and
@@ -378,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+      for (int dt = 0; dt < G::kBlocks; ++dt) {
         const V8 va = *reinterpret_cast<const V8*>(vt + vb.b[vt_operand_base_index(ks, dt)] +
                                                     vt_operand_offset(dt));
         o[dt] = mfma32(va, pb[ks], o[dt]);
@@ -386,6 +433,25 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
     }
   };
 
+  if constexpr (G::kRegSets == 1) {
+    // Tile it is computed from LDS buffer it % 2 while tile it + 1 is
+    // fetched into the one register set and stashed after the math.
+    Regs ra;
+    read_ids(kv_lo);
+    fetch(ra);
+    stash(0, ra);
+    read_ids(kv_lo + kTileKV);
+    __syncthreads();
+    for (int it = kv_lo / kTileKV; it < ntiles; ++it) {
+      const int n0 = it * kTileKV;
+      const int buf = (it - kv_lo / kTileKV) & 1;
+      if (it + 1 < ntiles) fetch(ra);
+      if (wave_active && n0 <= wave_last_pos) compute(buf, n0);
+      if (it + 1 < ntiles) stash(buf ^ 1, ra);   // buffer buf ^ 1 was last read before the previous barrier
+      read_ids(n0 + 2 * kTileKV);
+      __syncthreads();
+    }
+  } else {
   // Tile it is computed from LDS buffer it % 2 while tile it + 1 sits in
   // registers (loads issued one iteration earlier) and tile it + 2 is being
   // fetched into the other register set.
@@ -418,6 +484,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
       __syncthreads();
     }
   }
+  }
 
   lsum += __shfl_xor(lsum, 32);
   if (!row_ok) return;
@@ -425,7 +492,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   if (slot < 0) {
     f16* op = a.out + int64_t(qb + qrow) * a.o_tok + int64_t(hq) * a.o_head;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < G::kBlocks; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const V4 val = {T(o[dt][4 * g] * inv), T(o[dt][4 * g + 1] * inv),
@@ -436,10 +503,10 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(PrefillArgs a) 
   }
   // Split: this KV range's normalised O, its running max and its sum. A row
   // that sees no key of the range has sum 0 (weight 0 in the merge).
-  const int64_t prow = int64_t(slot) * kTileQ + (qrow - q0);
-  float* po = a.part_o + prow * kD;
+  const int64_t prow = int64_t(slot) * G::kTileQ + (qrow - q0);
+  float* po = a.part_o + prow * D;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < G::kBlocks; ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const f32x4 val = {o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
@@ -463,19 +530,20 @@ struct MergeArgs {
   int64_t o_tok, o_head;
 };
 
-// Grid (merge record, block of kMergeRows rows); one thread per (row, 8 dims).
-constexpr int kMergeRows = 256 / (kD / 8);
+// Grid (merge record, block of merge_rows(D) rows); one thread per (row, 8 dims).
+constexpr int merge_rows(int head_dim) { return 256 / (head_dim / 8); }
 
-template <typename T>
+template <typename T, int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(MergeArgs a) {
   typedef typename Vec<T>::v4 V4;
+  constexpr int kTileQ = Geom<D>::kTileQ;
   const int32_t* rec = a.merges + kMergeRec * blockIdx.x;
   const int seq = rec[0], q0 = rec[1], hq = rec[2], s0 = rec[3], n = rec[4];
   const int qb = a.q_indptr[seq];
   const int q_len = a.q_indptr[seq + 1] - qb;
   {
-    const int row = blockIdx.y * kMergeRows + int(threadIdx.x) / (kD / 8);
-    const int c = int(threadIdx.x) % (kD / 8);
+    const int row = blockIdx.y * merge_rows(D) + int(threadIdx.x) / (D / 8);
+    const int c = int(threadIdx.x) % (D / 8);
     if (q0 + row >= q_len) return;
     float mx = -INFINITY;
     for (int j = 0; j < n; ++j) {
@@ -489,8 +557,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MergeArgs a) {
       if (!(l > 0.f)) continue;
       const float w = fast_exp2(a.part_ml[2 * pr] - mx) * l;
       wsum += w;
-      const f32x4 x0 = *reinterpret_cast<const f32x4*>(a.part_o + pr * kD + 8 * c);
-      const f32x4 x1 = *reinterpret_cast<const f32x4*>(a.part_o + pr * kD + 8 * c + 4);
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(a.part_o + pr * D + 8 * c);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(a.part_o + pr * D + 8 * c + 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         acc[e] = fmaf(w, x0[e], acc[e]);
@@ -669,20 +737,31 @@ __global__ __launch_bounds__(kRopeThreads) void rope_append_kernel(RopeArgs a) {
 }
 
 // Attention (page ids staged in LDS when they fit), then the split merge.
-template <typename T>
+template <typename T, int D>
 int run_prefill(const PrefillArgs& a, const MergeArgs& m, int num_tiles, int num_merge,
                 bool staged, hipStream_t s) {
+  constexpr int kThreads = Geom<D>::kThreads;
   if (staged) {
-    paged_prefill_kernel<T, true><<<dim3(num_tiles), kThreads, 0, s>>>(a);
+    paged_prefill_kernel<T, D, true><<<dim3(num_tiles), kThreads, 0, s>>>(a);
   } else {
-    paged_prefill_kernel<T, false><<<dim3(num_tiles), kThreads, 0, s>>>(a);
+    paged_prefill_kernel<T, D, false><<<dim3(num_tiles), kThreads, 0, s>>>(a);
   }
   KSV_CHECK_LAUNCH();
   if (num_merge > 0) {
-    prefill_merge_kernel<T><<<dim3(num_merge, kTileQ / kMergeRows), 256, 0, s>>>(m);
+    prefill_merge_kernel<T, D><<<dim3(num_merge, Geom<D>::kTileQ / merge_rows(D)), 256, 0, s>>>(m);
     KSV_CHECK_LAUNCH();
   }
   return KUNSERVE_OK;
+}
+
+template <typename T>
+int run_prefill_dim(int head_dim, const PrefillArgs& a, const MergeArgs& m, int num_tiles,
+                    int num_merge, bool staged, hipStream_t s) {
+  switch (head_dim) {
+    case 64: return run_prefill<T, 64>(a, m, num_tiles, num_merge, staged, s);
+    case 128: return run_prefill<T, 128>(a, m, num_tiles, num_merge, staged, s);
+    default: return run_prefill<T, 256>(a, m, num_tiles, num_merge, staged, s);
+  }
 }
 
 }  // namespace
@@ -804,20 +883,28 @@ extern "C" int kunserve_append_kv(const kunserve_kv_pool* pool, int32_t layer,
 
 // Splits: a step with fewer q-tile workgroups than CUs splits the KV range
 // of its tiles into about kSplitWaves workgroups per CU, each covering at
-// least kMinSplitTiles KV tiles (a multiple of kTileKV). One: a CU holds
-// one workgroup at a time (78 KiB of LDS, 512 threads), so the splits run
-// in a single round (measured on the chunked-prefill workload's last step:
-// 0.047 ms, against 0.065 ms with two per CU and 0.077 ms with three).
+// least kMinSplitTiles KV tiles (a multiple of kTileKV). One: at head_dim
+// 128 a CU holds one workgroup at a time (76 KiB of LDS, 512 threads), so
+// the splits run in a single round (measured on the chunked-prefill
+// workload's last step: 0.047 ms, against 0.065 ms with two per CU and
+// 0.077 ms with three).
 constexpr int kSplitWaves = 1;
 constexpr int kMinSplitTiles = 4;
 constexpr int kMaxSplitItems = 2 * 1024;   // upper bound of the split target
 
+static bool prefill_head_dim_ok(int32_t head_dim) {
+  return head_dim == 64 || head_dim == 128 || head_dim == 256;
+}
+
 extern "C" int64_t kunserve_prefill_plan_bound(const int32_t* q_indptr_host, int32_t num_seqs,
-                                               int32_t num_qo_heads) {
-  if (num_seqs < 0 || num_qo_heads <= 0 || (num_seqs > 0 && !q_indptr_host)) return -1;
+                                               int32_t num_qo_heads, int32_t head_dim) {
+  if (num_seqs < 0 || num_qo_heads <= 0 || (num_seqs > 0 && !q_indptr_host) ||
+      !prefill_head_dim_ok(head_dim))
+    return -1;
+  const int32_t tile_q = tile_q_for(head_dim);
   int64_t tiles = 0;
   for (int32_t b = 0; b < num_seqs; ++b)
-    tiles += (std::max(q_indptr_host[b + 1] - q_indptr_host[b], 0) + kTileQ - 1) / kTileQ;
+    tiles += (std::max(q_indptr_host[b + 1] - q_indptr_host[b], 0) + tile_q - 1) / tile_q;
   const int64_t items = tiles * num_qo_heads;
   // Splitting adds at most kMaxSplitItems workgroups; worst case every item
   // on one XCD and the others padded to the same depth; one merge record per
@@ -827,10 +914,16 @@ extern "C" int64_t kunserve_prefill_plan_bound(const int32_t* q_indptr_host, int
 
 extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t* kv_len_host,
                                      int32_t num_seqs, int32_t num_qo_heads,
-                                     int32_t num_kv_heads, int32_t num_cus, int32_t* plan_host,
-                                     int64_t plan_capacity, kunserve_prefill_plan_info* info) {
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t num_cus,
+                                     int32_t* plan_host, int64_t plan_capacity,
+                                     kunserve_prefill_plan_info* info) {
   clear_error();
   KSV_CHECK_ARG(info && plan_host && num_seqs >= 0, "bad argument");
+  if (!prefill_head_dim_ok(head_dim)) {
+    set_error("prefill supports head_dim 64, 128 and 256, got %d", head_dim);
+    return KUNSERVE_EUNSUPPORTED;
+  }
+  const int32_t tile_q = tile_q_for(head_dim);
   KSV_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && num_qo_heads % num_kv_heads == 0,
                 "num_qo_heads %d not a multiple of num_kv_heads %d", num_qo_heads, num_kv_heads);
   KSV_CHECK_ARG(num_cus >= 0, "num_cus %d < 0", num_cus);
@@ -849,9 +942,9 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
     if (ql == 0) continue;
     n_pairs += num_kv_heads;
     const int32_t prefix = kv_len_host[b] - ql;
-    for (int32_t q0 = 0; q0 < ql; q0 += kTileQ) {
+    for (int32_t q0 = 0; q0 < ql; q0 += tile_q) {
       n_items += num_qo_heads;
-      kv_units += int64_t(num_qo_heads) * ((prefix + std::min(q0 + kTileQ, ql) + kTileKV - 1) / kTileKV);
+      kv_units += int64_t(num_qo_heads) * ((prefix + std::min(q0 + tile_q, ql) + kTileKV - 1) / kTileKV);
     }
   }
   // KV tiles per split (0: no split).
@@ -867,15 +960,15 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
     if (ql == 0) continue;
     const int32_t prefix = kv_len_host[b] - ql;
     auto tile_cost = [&](int32_t q0) {
-      return (int64_t(prefix) + std::min(q0 + kTileQ, ql)) * ratio;
+      return (int64_t(prefix) + std::min(q0 + tile_q, ql)) * ratio;
     };
     for (int32_t g = 0; g < num_kv_heads; ++g) {
       if (split_tiles) {
-        for (int32_t q0 = 0; q0 < ql; q0 += kTileQ)
-          groups.push_back({b, g, q0, std::min(q0 + kTileQ, ql), tile_cost(q0)});
+        for (int32_t q0 = 0; q0 < ql; q0 += tile_q)
+          groups.push_back({b, g, q0, std::min(q0 + tile_q, ql), tile_cost(q0)});
       } else {
         int64_t cost = 0;
-        for (int32_t q0 = 0; q0 < ql; q0 += kTileQ) cost += tile_cost(q0);
+        for (int32_t q0 = 0; q0 < ql; q0 += tile_q) cost += tile_cost(q0);
         groups.push_back({b, g, 0, ql, cost});
       }
     }
@@ -893,16 +986,16 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
     load[x] += g.cost;
     const int32_t ql = q_indptr_host[g.seq + 1] - q_indptr_host[g.seq];
     const int32_t prefix = kv_len_host[g.seq] - ql;
-    auto tile_end = [&](int32_t q0) { return prefix + std::min(q0 + kTileQ, ql); };
+    auto tile_end = [&](int32_t q0) { return prefix + std::min(q0 + tile_q, ql); };
     auto n_splits = [&](int32_t q0) {
       const int64_t units = (tile_end(q0) + kTileKV - 1) / kTileKV;
       return chunk > 0 ? int32_t((units + chunk - 1) / chunk) : 1;
     };
     int32_t max_splits = 1;
-    for (int32_t q0 = g.t0; q0 < g.t1; q0 += kTileQ) max_splits = std::max(max_splits, n_splits(q0));
+    for (int32_t q0 = g.t0; q0 < g.t1; q0 += tile_q) max_splits = std::max(max_splits, n_splits(q0));
     // First slot of each (tile, head) that is split.
     std::vector<int32_t> first_slot;
-    for (int32_t q0 = g.t0; q0 < g.t1; q0 += kTileQ) {
+    for (int32_t q0 = g.t0; q0 < g.t1; q0 += tile_q) {
       const int32_t n = n_splits(q0);
       for (int32_t hq = g.hkv * ratio; hq < (g.hkv + 1) * ratio; ++hq) {
         first_slot.push_back(n > 1 ? slots : -1);
@@ -914,7 +1007,7 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
     }
     for (int32_t j = 0; j < max_splits; ++j) {
       size_t k = 0;
-      for (int32_t q0 = g.t0; q0 < g.t1; q0 += kTileQ) {
+      for (int32_t q0 = g.t0; q0 < g.t1; q0 += tile_q) {
         const int32_t n = n_splits(q0);
         for (int32_t hq = g.hkv * ratio; hq < (g.hkv + 1) * ratio; ++hq, ++k) {
           if (j >= n) continue;
@@ -947,7 +1040,8 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
     }
   std::copy(merges.begin(), merges.end(), plan_host + int64_t(kRec) * depth * kXcds);
   info->num_tiles = int32_t(depth * kXcds);
-  info->tile_q = kTileQ;
+  info->tile_q = tile_q;
+  info->head_dim = head_dim;
   info->plan_ints = int32_t(need);
   info->num_qo_heads = num_qo_heads;
   int32_t max_kv = 0;
@@ -964,7 +1058,7 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
 
 extern "C" int64_t kunserve_prefill_workspace_bytes(const kunserve_prefill_plan_info* info) {
   if (!info) return -1;
-  return int64_t(info->num_slots) * kTileQ * (kD + 2) * int64_t(sizeof(float));
+  return int64_t(info->num_slots) * info->tile_q * (info->head_dim + 2) * int64_t(sizeof(float));
 }
 
 extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
@@ -983,15 +1077,16 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
                 pool->num_layers);
   KSV_CHECK_ARG(std::isfinite(sm_scale) && sm_scale > 0.f,
                 "sm_scale %g must be finite and positive", double(sm_scale));
-  if (pool->head_dim != kD) {
-    set_error("prefill kernel is compiled for head_dim %d, got %d", kD, pool->head_dim);
+  if (!prefill_head_dim_ok(pool->head_dim)) {
+    set_error("prefill supports head_dim 64, 128 and 256, got %d", pool->head_dim);
     return KUNSERVE_EUNSUPPORTED;
   }
   KSV_CHECK_ARG(num_qo_heads > 0 && num_qo_heads % pool->num_kv_heads == 0,
                 "num_qo_heads %d not a multiple of num_kv_heads %d", num_qo_heads,
                 pool->num_kv_heads);
-  KSV_CHECK_ARG(info->tile_q == kTileQ, "plan tile %d does not match kernel tile %d",
-                info->tile_q, kTileQ);
+  KSV_CHECK_ARG(info->head_dim == pool->head_dim && info->tile_q == tile_q_for(pool->head_dim),
+                "plan made for head_dim %d (tile %d), pool has head_dim %d", info->head_dim,
+                info->tile_q, pool->head_dim);
   KSV_CHECK_ARG(info->num_qo_heads == num_qo_heads, "plan made for %d q heads, called with %d",
                 info->num_qo_heads, num_qo_heads);
   if (info->num_tiles == 0) return KUNSERVE_OK;
@@ -1037,7 +1132,8 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   a.q_indptr = q_indptr_dev;
   a.tiles = plan_dev;
   a.part_o = static_cast<float*>(workspace_dev);
-  a.part_ml = a.part_o ? a.part_o + int64_t(info->num_slots) * kTileQ * kD : nullptr;
+  a.part_ml = a.part_o ? a.part_o + int64_t(info->num_slots) * info->tile_q * pool->head_dim
+                       : nullptr;
   a.ratio = num_qo_heads / pool->num_kv_heads;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   const int64_t pages_needed = (int64_t(info->max_kv_len) + pool->page_size - 1) / pool->page_size;
@@ -1051,8 +1147,8 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   m.o_head = a.o_head;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (pool->dtype == KUNSERVE_DTYPE_BF16)
-    return run_prefill<bf16>(a, m, info->num_tiles, info->num_merge,
+    return run_prefill_dim<bf16>(pool->head_dim, a, m, info->num_tiles, info->num_merge,
                              pages_needed <= kMaxStagedPages, s);
-  return run_prefill<f16>(a, m, info->num_tiles, info->num_merge, pages_needed <= kMaxStagedPages,
-                          s);
+  return run_prefill_dim<f16>(pool->head_dim, a, m, info->num_tiles, info->num_merge,
+                              pages_needed <= kMaxStagedPages, s);
 }

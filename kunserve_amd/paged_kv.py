@@ -348,18 +348,21 @@ class PrefillPlan:
 
     def __init__(self, q_indptr_host: Sequence[int], kv_len_host: Sequence[int],
                  num_qo_heads: int, num_kv_heads: int, device: torch.device,
-                 num_cus: Optional[int] = None, upload: bool = True):
+                 num_cus: Optional[int] = None, upload: bool = True, head_dim: int = 128):
+        """head_dim: the pool's (64, 128 or 256); it sets the plan's tile."""
         qi = _i32(q_indptr_host)
         kv = _i32(kv_len_host)
         n = len(kv)
         if len(qi) != n + 1:
             raise ValueError("q_indptr must have num_seqs + 1 entries")
-        cap = int(_lib.lib().kunserve_prefill_plan_bound(qi.ctypes.data, n, num_qo_heads))
+        cap = int(_lib.lib().kunserve_prefill_plan_bound(qi.ctypes.data, n, num_qo_heads,
+                                                         head_dim))
+        # A negative bound (bad arguments) leaves the plan call to report them.
         buf = np.zeros(max(cap, 3), dtype=np.int32)
         self.info = _lib.PrefillPlanInfo()
         cus = num_cus if num_cus is not None else _num_cus(device)
         _lib.call("kunserve_prefill_plan", qi.ctypes.data, kv.ctypes.data if n else None, n,
-                  num_qo_heads, num_kv_heads, cus, buf.ctypes.data, buf.size,
+                  num_qo_heads, num_kv_heads, head_dim, cus, buf.ctypes.data, buf.size,
                   ctypes.byref(self.info))
         self.plan_host = buf[: self.info.plan_ints].copy()
         self.plan = None
@@ -643,7 +646,7 @@ class AttentionStep:
                 qi = np.zeros(pre_rows.size + 1, dtype=np.int32)
                 np.cumsum(q_lens[pre_rows], out=qi[1:])
             plan = PrefillPlan(qi, self.kv_len[pre_rows], num_qo_heads, pool.num_kv_heads, dev,
-                               upload=False)
+                               upload=False, head_dim=pool.head_dim)
             self.prefill = _Subset(pre_rows, tokens, table, None, plan)
             uploads += ([] if whole else [table, [tokens], [qi]]) + [plan]
 

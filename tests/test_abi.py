@@ -77,12 +77,13 @@ def test_decode_plan_rejects_bad_arguments():
     assert e.value.code == _lib.ENOSPC
 
 
-def _prefill_plan(q_indptr, kv, hq, hkv, num_cus=256):
-    cap = _lib.lib().kunserve_prefill_plan_bound(q_indptr.ctypes.data, len(kv), hq)
+def _prefill_plan(q_indptr, kv, hq, hkv, num_cus=256, head_dim=128):
+    cap = _lib.lib().kunserve_prefill_plan_bound(q_indptr.ctypes.data, len(kv), hq, head_dim)
     buf = np.full(cap, -7, dtype=np.int32)
     info = _lib.PrefillPlanInfo()
     _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, kv.ctypes.data, len(kv), hq, hkv,
-              num_cus, buf.ctypes.data, cap, ctypes.byref(info))
+              head_dim, num_cus, buf.ctypes.data, cap, ctypes.byref(info))
+    assert info.head_dim == head_dim
     items = buf[:6 * info.num_tiles].reshape(-1, 6)
     merges = buf[6 * info.num_tiles:info.plan_ints].reshape(-1, 5)
     return info, items, merges
@@ -121,16 +122,18 @@ def _check_prefill_plan(q_indptr, q_lens, kv, hq, hkv, info, items, merges):
             slots += [r[2] for r in rs]
     assert sorted(slots) == list(range(info.num_slots))
     ws = _lib.lib().kunserve_prefill_workspace_bytes(ctypes.byref(info))
-    assert ws == info.num_slots * tq * (128 + 2) * 4
+    assert ws == info.num_slots * tq * (info.head_dim + 2) * 4
 
 
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
 @pytest.mark.parametrize("hq,hkv,n", [(4, 4, 3), (8, 2, 3), (32, 32, 16), (1, 1, 1)])
-def test_prefill_plan_covers_every_tile_once(hq, hkv, n):
+def test_prefill_plan_covers_every_tile_once(hq, hkv, n, head_dim):
     rng = np.random.default_rng(hq + n)
     q_lens = rng.integers(0, 900, n)
     q_indptr = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
     kv = (q_lens + rng.integers(0, 3000, n)).astype(np.int32)
-    info, items, merges = _prefill_plan(q_indptr, kv, hq, hkv)
+    info, items, merges = _prefill_plan(q_indptr, kv, hq, hkv, head_dim=head_dim)
+    assert info.tile_q == (128 if head_dim == 256 else 256)
     _check_prefill_plan(q_indptr, q_lens, kv, hq, hkv, info, items, merges)
     # items that read the same K/V (row, KV head) sit on one XCD
     xcd = {}
@@ -172,8 +175,21 @@ def test_prefill_plan_rejects_short_kv():
     buf = np.zeros(64, dtype=np.int32)
     info = _lib.PrefillPlanInfo()
     with pytest.raises(_lib.KunserveError):
-        _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, bad.ctypes.data, 3, 4, 4, 0,
-                  buf.ctypes.data, 64, ctypes.byref(info))
+        _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, bad.ctypes.data, 3, 4, 4, 128,
+                  0, buf.ctypes.data, 64, ctypes.byref(info))
+
+
+@pytest.mark.parametrize("head_dim", [32, 96, 512])
+def test_prefill_plan_rejects_unsupported_head_dims(head_dim):
+    q_indptr = np.array([0, 8], dtype=np.int32)
+    kv = np.array([8], dtype=np.int32)
+    assert _lib.lib().kunserve_prefill_plan_bound(q_indptr.ctypes.data, 1, 4, head_dim) == -1
+    buf = np.zeros(64, dtype=np.int32)
+    info = _lib.PrefillPlanInfo()
+    with pytest.raises(_lib.KunserveError) as e:
+        _lib.call("kunserve_prefill_plan", q_indptr.ctypes.data, kv.ctypes.data, 1, 4, 4,
+                  head_dim, 0, buf.ctypes.data, 64, ctypes.byref(info))
+    assert e.value.code == _lib.EUNSUPPORTED
 
 
 def test_swap_rejects_out_of_range_ids_before_any_copy():

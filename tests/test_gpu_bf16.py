@@ -49,22 +49,25 @@ def test_bf16_decode_matches_oracle(device, head_dim, hq, hkv):
 
 
 @pytest.mark.parametrize("num_cus", [1, 1024])
-def test_bf16_prefill_matches_oracle(device, num_cus):
-    """Whole KV ranges (num_cus 1) and split ones (num_cus 1024)."""
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_bf16_prefill_matches_oracle(device, num_cus, head_dim):
+    """Whole KV ranges (num_cus 1) and split ones (num_cus 1024), head_dim
+    64, 128 and 256."""
     rng = np.random.default_rng(num_cus)
     q_lens, prefixes = [1, 77, 256, 300, 512], [700, 0, 1500, 33, 2048]
     kv = np.asarray(q_lens) + np.asarray(prefixes)
     kv, indptr, indices = rows_csr(rng, kv, 16, 600)
     q_indptr = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
-    pool = random_pool(600, 1, 4, 16, 128, device, 3, dtype=BF16)
-    q = random_tensor((int(q_indptr[-1]), 8, 128), device, 4, dtype=BF16)
-    plan = PrefillPlan(q_indptr, kv, 8, 4, device, num_cus=num_cus)
+    pool = random_pool(600, 1, 4, 16, head_dim, device, 3, dtype=BF16)
+    q = random_tensor((int(q_indptr[-1]), 8, head_dim), device, 4, dtype=BF16)
+    plan = PrefillPlan(q_indptr, kv, 8, 4, device, num_cus=num_cus, head_dim=head_dim)
     assert (plan.info.num_merge > 0) == (num_cus == 1024)
     out = paged_prefill(pool, 0, table_from_csr(indptr, indices, kv, device),
                         torch.from_numpy(q_indptr).to(device), q, plan)
     torch.cuda.synchronize()
     k, v, ip, ix = compact_for_oracle(pool, 0, indptr, indices)
-    want = ref.prefill_attention(to_numpy(q), q_indptr, k, v, 0, ip, ix, kv, 1 / math.sqrt(128))
+    want = ref.prefill_attention(to_numpy(q), q_indptr, k, v, 0, ip, ix, kv,
+                                 1 / math.sqrt(head_dim))
     assert max_abs(out, want) <= ATOL_BF16
     assert rel_err(out, want) <= RTOL_BF16, rel_err(out, want)
 

@@ -45,7 +45,7 @@ def run_prefill(pool, layer, q_lens, kv, indptr, indices, q_indptr, hq, device, 
     T = int(q_indptr[-1])
     q = random_tensor((T, hq, pool.head_dim), device, seed)
     table = table_from_csr(indptr, indices, kv, device)
-    plan = PrefillPlan(q_indptr, kv, hq, pool.num_kv_heads, device)
+    plan = PrefillPlan(q_indptr, kv, hq, pool.num_kv_heads, device, head_dim=pool.head_dim)
     out = paged_prefill(pool, layer, table, torch.from_numpy(q_indptr).to(device), q, plan)
     torch.cuda.synchronize()
     return q, out
@@ -69,6 +69,58 @@ def test_prefill_matches_oracle(device, hq, hkv, ps):
     q, out = run_prefill(pool, 1, q_lens, kv, indptr, indices, q_indptr, hq, device, 6)
     want = oracle_prefill(pool, 1, q, q_indptr, indptr, indices, kv)
     assert max_abs(out, want) <= ATOL
+
+
+@pytest.mark.parametrize("head_dim", [64, 256])
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 2)])
+@pytest.mark.parametrize("cus", [None, 1024])
+def test_prefill_head_dims_match_oracle(device, head_dim, hq, hkv, cus):
+    """head_dim 64 (8 waves, two per SIMD) and 256 (4 waves of 128-row
+    tiles, one per SIMD): whole KV ranges and, with a plan made for 1024
+    CUs, split ones plus the merge; ragged rows with prefixes."""
+    rng = np.random.default_rng(head_dim + hq + hkv)
+    q_lens = [1, 5, 64, 127, 128, 129, 300, 512]
+    prefixes = [0, 17, 0, 100, 1000, 3, 64, 2048]
+    kv, indptr, indices, q_indptr = make_rows(rng, q_lens, prefixes, 16, 400)
+    pool = random_pool(400, 2, hkv, 16, head_dim, device, 50 + head_dim)
+    q = random_tensor((int(q_indptr[-1]), hq, head_dim), device, 51)
+    table = table_from_csr(indptr, indices, kv, device)
+    plan = PrefillPlan(q_indptr, kv, hq, hkv, device, num_cus=cus, head_dim=head_dim)
+    assert plan.info.tile_q == (128 if head_dim == 256 else 256)
+    if cus == 1024:
+        assert plan.info.num_merge > 0
+    out = paged_prefill(pool, 1, table, torch.from_numpy(q_indptr).to(device), q, plan)
+    torch.cuda.synchronize()
+    want = oracle_prefill(pool, 1, q, q_indptr, indptr, indices, kv)
+    assert max_abs(out, want) <= ATOL
+
+
+@pytest.mark.parametrize("head_dim", [64, 256])
+def test_prefill_head_dims_long_row_unstaged_ids(device, head_dim):
+    """A row with more pages than the kernel stages in LDS (page size 4,
+    9000 cached tokens) reads its page ids from the table, at head_dim 64
+    and 256."""
+    rng = np.random.default_rng(head_dim)
+    q_lens, prefixes = [100, 40], [8900, 30]
+    kv, indptr, indices, q_indptr = make_rows(rng, q_lens, prefixes, 4, 2400)
+    pool = random_pool(2400, 1, 2, 4, head_dim, device, 60)
+    q, out = run_prefill(pool, 0, q_lens, kv, indptr, indices, q_indptr, 4, device, 61)
+    want = oracle_prefill(pool, 0, q, q_indptr, indptr, indices, kv)
+    assert max_abs(out, want) <= ATOL
+
+
+def test_prefill_plan_for_another_head_dim_is_rejected(device):
+    from kunserve_amd._lib import EINVAL, KunserveError
+
+    rng = np.random.default_rng(3)
+    kv, indptr, indices, q_indptr = make_rows(rng, [10], [5], 16, 8)
+    pool = random_pool(8, 1, 2, 16, 64, device, 62)
+    q = random_tensor((10, 2, 64), device, 63)
+    plan = PrefillPlan(q_indptr, kv, 2, 2, device)          # made for head_dim 128
+    with pytest.raises(KunserveError) as e:
+        paged_prefill(pool, 0, table_from_csr(indptr, indices, kv, device),
+                      torch.from_numpy(q_indptr).to(device), q, plan)
+    assert e.value.code == EINVAL
 
 
 @pytest.mark.parametrize("ps", [16, 64])
@@ -189,10 +241,11 @@ def test_chunked_prefill_workload_sampled(device):
             assert max_abs(out, want) <= ATOL
 
 
-def test_attention_step_mixed_batch(device):
+@pytest.mark.parametrize("head_size", [64, 128, 256])
+def test_attention_step_mixed_batch(device, head_size):
     """One pforward step with prefill and decode rows interleaved: append of
     every row's new tokens, then decode and prefill attention."""
-    op = LlamaOp(256, 2, 8, 4, 16, 128, 1, 1, 8, 4096, 4096, 1, device)
+    op = LlamaOp(256, 2, 8, 4, 16, head_size, 1, 1, 8, 4096, 4096, 1, device)
     op.pool.k.copy_(random_tensor(op.pool.k.shape, device, 1))
     op.pool.v.copy_(random_tensor(op.pool.v.shape, device, 2))
     rng = np.random.default_rng(3)
@@ -211,9 +264,9 @@ def test_attention_step_mixed_batch(device):
     tokens = [list(range(n)) for n in q_lens]
     step = op.pforward(4, sum(q_lens), 256, 0, 2, tokens, first, flags, pages, 0, [], [], 0)
     T = sum(q_lens)
-    q = random_tensor((T, 8, 128), device, 4)
-    k = random_tensor((T, 4, 128), device, 5)
-    v = random_tensor((T, 4, 128), device, 6)
+    q = random_tensor((T, 8, head_size), device, 4)
+    k = random_tensor((T, 4, head_size), device, 5)
+    v = random_tensor((T, 4, head_size), device, 6)
     k_host, v_host = op.pool.k.cpu().numpy(), op.pool.v.cpu().numpy()
     out = step.run(1, q, k, v)
     torch.cuda.synchronize()
@@ -224,7 +277,7 @@ def test_attention_step_mixed_batch(device):
                   v.cpu().numpy())
     assert np.array_equal(op.pool.k.cpu().numpy().view(np.int16), k_host.view(np.int16))
     want = ref.prefill_attention(q.cpu().numpy(), q_indptr, k_host, v_host, 1, indptr, indices,
-                                 np.array(kv), 1 / math.sqrt(128))
+                                 np.array(kv), 1 / math.sqrt(head_size))
     assert max_abs(out, want) <= ATOL
     assert step.decode is not None and step.prefill is not None
 

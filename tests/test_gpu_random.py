@@ -57,25 +57,25 @@ def test_decode_random_cases(device, hkv, ratio, d, ps, kv, part, bf16, seed):
 
 @RANDOM
 @given(hkv=st.sampled_from([1, 2, 4]), ratio=st.sampled_from([1, 2, 4]),
-       ps=st.sampled_from([4, 16, 64, 256]),
+       d=st.sampled_from([64, 128, 256]), ps=st.sampled_from([4, 16, 64, 256]),
        rows=st.lists(st.tuples(st.integers(1, 200), st.integers(0, 800)), min_size=1,
                      max_size=4),
        bf16=st.booleans(), seed=st.integers(0, 2**16))
-def test_prefill_random_cases(device, hkv, ratio, ps, rows, bf16, seed):
+def test_prefill_random_cases(device, hkv, ratio, d, ps, rows, bf16, seed):
     dtype = torch.bfloat16 if bf16 else torch.float16
     rng = np.random.default_rng(seed)
     q_lens = np.array([r[0] for r in rows], dtype=np.int32)
     kv, indptr, indices, npg = _rows(rng, [q + p for q, p in rows], ps)
     q_indptr = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
     hq = hkv * ratio
-    pool = random_pool(npg, 1, hkv, ps, 128, device, seed, dtype=dtype)
-    q = random_tensor((int(q_indptr[-1]), hq, 128), device, seed + 1, dtype=dtype)
-    plan = PrefillPlan(q_indptr, kv, hq, hkv, device)
+    pool = random_pool(npg, 1, hkv, ps, d, device, seed, dtype=dtype)
+    q = random_tensor((int(q_indptr[-1]), hq, d), device, seed + 1, dtype=dtype)
+    plan = PrefillPlan(q_indptr, kv, hq, hkv, device, head_dim=d)
     out = paged_prefill(pool, 0, table_from_csr(indptr, indices, kv, device),
                         torch.from_numpy(q_indptr).to(device), q, plan)
     torch.cuda.synchronize()
     k, v, ip, ix = compact_for_oracle(pool, 0, indptr, indices)
-    want = ref.prefill_attention(to_numpy(q), q_indptr, k, v, 0, ip, ix, kv, 1 / math.sqrt(128))
+    want = ref.prefill_attention(to_numpy(q), q_indptr, k, v, 0, ip, ix, kv, 1 / math.sqrt(d))
     assert max_abs(out, want) <= (ATOL_BF16 if bf16 else ATOL)
 
 
