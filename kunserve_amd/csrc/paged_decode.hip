@@ -545,8 +545,7 @@ __global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merg
       const float w = j < n ? fast_exp2(part_lse[int64_t(s0 + j) * num_qo_heads + hq] - mx) : 0.f;
       wsum += w;
       const int cnt = min(kWave, n - base);
-#pragma unroll 4
-      for (int t = 0; t < cnt; ++t) {
+      for (int t = 0; t < cnt; ++t) {   // not unrollable: __shfl is convergent
         const float wt = __shfl(w, t);
         const float* src = part_o + (int64_t(s0 + base + t) * num_qo_heads + hq) * D + lane * DPL;
 #pragma unroll
