@@ -247,6 +247,18 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   const int kv_end = min(prefix + min(q0 + G::kTileQ, q_len), kv_hi);   // exclusive
   const int ntiles = (kv_end + kTileKV - 1) / kTileKV;   // tiles [kv_lo / kTileKV, ntiles)
   const int pg_lo = kv_lo >> a.page_shift;   // first staged page
+  // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
+  // Issued before the page-id staging, so that both loads' latencies
+  // overlap, and with no branch: a row past q_len reads the sequence's
+  // first row instead (its scores stay in its own lane column, and it
+  // writes no output).
+  V8 qf[G::kSteps];
+  {
+    const f16* qp = a.q + int64_t(qb + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
+#pragma unroll
+    for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
+  }
+
   // Stage (or, for rows with too many pages, only scan) the page ids of
   // [kv_lo, kv_end). Whether any of them is outside the pool is voted per
   // wave: only then do the scores need a per-page mask, which drops the
@@ -274,14 +286,6 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
     const int p = STAGED ? s_pg[(tok >> a.page_shift) - pg_lo] : pages[tok >> a.page_shift];
     return uint32_t(p) >= uint32_t(a.num_pages);
   };
-
-  // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
-  V8 qf[G::kSteps];
-  {
-    const f16* qp = a.q + int64_t(qb + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
-#pragma unroll
-    for (int s = 0; s < G::kSteps; ++s) qf[s] = row_ok ? load_v8<T>(qp + 16 * s + 8 * h) : V8{};
-  }
 
   f32x16 o[G::kBlocks];
 #pragma unroll
