@@ -523,6 +523,359 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   }
 }
 
+// Warp-specialised variant for head_dim 64 and 128. A workgroup is 12
+// waves: compute waves 0-7 (32 query rows each, two per SIMD) only read
+// LDS and run the math; loader waves 8-11 (one per SIMD) only gather K/V
+// tiles from the pages into LDS. Loaders run one tile ahead: tile u is
+// written between barriers u - 2 and u - 1, into K buffer u % 2 and V
+// buffer u % 3, from registers loaded two tiles earlier. Compute waves run
+// barrier t between the two 32-token halves of tile t (the second half's
+// score MFMAs read K of tile t + 1, published by that barrier). The
+// interior tiles, whose keys every row sees, run a straight-line pipeline
+// (the scores of half-step j + 1 issue between the exponentials of j, and
+// the P.V of j beside the max of j + 1); the diagonal tiles run each half
+// on its own, with the causal / past-the-end / bad-page masks.
+template <int D>
+struct WsGeom {
+  static_assert(D == 64 || D == 128, "warp-specialised prefill is for head_dim 64 and 128");
+  static constexpr int kComputeWaves = 8;
+  static constexpr int kLoadWaves = 4;
+  static constexpr int kWaves = kComputeWaves + kLoadWaves;
+  static constexpr int kThreads = kWaves * kWave;
+  static constexpr int kTileQ = 32 * kComputeWaves;
+  static constexpr int kSteps = D / 16;
+  static constexpr int kBlocks = D / 32;
+  static constexpr int kKPitch = D + 8;
+  static constexpr int kKHalves = kTileKV * kKPitch;
+  static constexpr int kVtHalves = D * kVtPitch;
+  // Units (4 tokens x 8 dims of K or V) per loader lane: at 128 each loader
+  // wave gathers V and K of one token group of 16 (the same lane layout for
+  // both); at 64 loaders 0-1 gather V and 2-3 K, two token groups a wave.
+  static constexpr int kUnits = D == 128 ? 2 : 1;
+};
+
+template <typename T, int D, bool STAGED>
+__global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(PrefillArgs a) {
+  typedef typename Vec<T>::v8 V8;
+  typedef WsGeom<D> G;
+  __shared__ int s_pg[STAGED ? kMaxStagedPages : 1];
+  __shared__ int s_bad[G::kWaves];
+  __shared__ __attribute__((aligned(16))) T sK[2 * G::kKHalves];
+  __shared__ __attribute__((aligned(16))) T sVt[3 * G::kVtHalves];
+
+  const int32_t* item = a.tiles + kRec * blockIdx.x;
+  const int seq = item[0];
+  if (seq < 0) return;   // padding workgroup (uniform: no barrier reached)
+  const int q0 = item[1];
+  const int hq = item[2];
+  const int kv_lo = item[3];   // a multiple of kTileKV
+  const int kv_hi = item[4];
+  const int slot = item[5];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool loader = wave >= G::kComputeWaves;   // uniform per wave
+  const int r = lane & 31;
+  const int h = lane >> 5;
+
+  const int hkv = hq / a.ratio;
+  const int qb = a.q_indptr[seq];
+  const int q_len = a.q_indptr[seq + 1] - qb;
+  const int kvl = a.kv_len[seq];
+  const int prefix = kvl - q_len;
+  const int32_t* pages = a.indices + a.indptr[seq];
+  const int page_mask = (1 << a.page_shift) - 1;
+  const int kv_end = min(prefix + min(q0 + G::kTileQ, q_len), kv_hi);   // exclusive
+  const int ntiles = (kv_end + kTileKV - 1) / kTileKV;   // tiles [kv_lo / kTileKV, ntiles)
+  const int t_first = kv_lo / kTileKV;
+  const int pg_lo = kv_lo >> a.page_shift;
+
+  // Stage (or, for rows with too many pages, only scan) the page ids of
+  // [kv_lo, kv_end) and vote whether any is outside the pool.
+  bool any_bad = false;
+  {
+    const int npg = kv_end > kv_lo ? ((kv_end - 1) >> a.page_shift) + 1 - pg_lo : 0;
+    bool bad_id = false;
+    for (int i = threadIdx.x; i < npg; i += G::kThreads) {
+      const int p = pages[pg_lo + i];
+      const bool ok = p >= 0 && p < a.num_pages;
+      if constexpr (STAGED) s_pg[i] = ok ? p : -1;
+      bad_id |= !ok;
+    }
+    const bool wave_bad = __any(bad_id);
+    if (lane == 0) s_bad[wave] = wave_bad;
+    __syncthreads();
+    int bad = 0;
+#pragma unroll
+    for (int wv = 0; wv < G::kWaves; ++wv) bad |= s_bad[wv];
+    any_bad = __builtin_amdgcn_readfirstlane(bad) != 0;
+  }
+  auto bad_page = [&](int tok) {
+    const int p = STAGED ? s_pg[(tok >> a.page_shift) - pg_lo] : pages[tok >> a.page_shift];
+    return uint32_t(p) >= uint32_t(a.num_pages);
+  };
+
+  if (loader) {
+    // ---------------------------------------------------------- loader
+    const int lw = wave - G::kComputeWaves;
+    const GatherLane gl = gather_lane<D>(D == 128 ? lw : lw % 2, lane);
+    const int ld_t = 16 * gl.g + 8 * gl.a + 4 * gl.h;
+    auto unit_v = [&](int u) { return D == 128 ? u == 0 : lw < 2; };
+    const f16* kbase = a.k + int64_t(hkv) * a.head_stride;
+    const f16* vbase = a.v + int64_t(hkv) * a.head_stride;
+    struct Regs {
+      V8 x[G::kUnits][4];
+      int nok;
+    };
+    TileAt at;
+    auto read_ids = [&](int n0) {
+      const int tok = n0 + ld_t;
+      const int t = max(kv_lo, min(tok, kv_end - 1));   // clamped into the staged range
+      const int p = STAGED ? s_pg[(t >> a.page_shift) - pg_lo] : pages[t >> a.page_shift];
+      at = tile_at(p, tok, kv_end, a.num_pages, a.page_stride, a.token_stride, page_mask, 8 * gl.c);
+    };
+    auto fetch = [&](Regs& rg) {
+#pragma unroll
+      for (int u = 0; u < G::kUnits; ++u) {
+        const f16* base = (unit_v(u) ? vbase : kbase) + at.off;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rg.x[u][i] = load_v8<T>(base + int64_t(i) * a.token_stride);
+      }
+      rg.nok = at.nok;
+    };
+    auto stash = [&](int kbuf, int vbuf, const Regs& rg) {
+#pragma unroll
+      for (int u = 0; u < G::kUnits; ++u) {
+        if (unit_v(u)) {
+#pragma unroll
+          for (int part = 0; part < 4; ++part)
+            vt_store<T>(sVt + vbuf * G::kVtHalves, gl, gl.c, rg.x[u], part, rg.nok);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<V8*>(&sK[kbuf * G::kKHalves + (ld_t + i) * G::kKPitch + 8 * gl.c]) =
+                rg.x[u][i];
+        }
+      }
+    };
+    // Tile t_first + k is in register set k % 2 (ra even, rb odd). The
+    // barrier after iteration u is barrier u - 1 of the compute waves.
+    Regs ra, rb;
+    read_ids(kv_lo);
+    fetch(ra);
+    read_ids(kv_lo + kTileKV);
+    fetch(rb);
+    stash(0, 0, ra);
+    read_ids(kv_lo + 2 * kTileKV);
+    fetch(ra);   // tile t_first + 2 (past the end: in-bounds reads, never stashed)
+    read_ids(kv_lo + 3 * kTileKV);
+    __syncthreads();
+    int kb = 1, vbn = 1;   // buffers of tile t_first + 1
+    auto advance = [&]() {
+      kb ^= 1;
+      vbn = vbn == 2 ? 0 : vbn + 1;
+    };
+    for (int u = t_first + 1; u <= ntiles; u += 2) {
+      if (u < ntiles) stash(kb, vbn, rb);
+      fetch(rb);   // tile u + 2
+      read_ids((u + 3) * kTileKV);
+      __syncthreads();
+      advance();
+      if (u + 1 > ntiles) break;
+      if (u + 1 < ntiles) stash(kb, vbn, ra);
+      fetch(ra);   // tile u + 3
+      read_ids((u + 4) * kTileKV);
+      __syncthreads();
+      advance();
+    }
+    return;
+  }
+
+  // ------------------------------------------------------------ compute
+  const int qrow = q0 + wave * 32 + r;
+  const bool row_ok = qrow < q_len;
+  const int qpos = prefix + qrow;
+  const bool wave_active = q0 + wave * 32 < q_len;
+  const int wave_last_pos = prefix + min(q0 + wave * 32 + 31, q_len - 1);
+  // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8
+  // (a row past q_len reads the sequence's first row and writes nothing).
+  V8 qf[G::kSteps];
+  {
+    const f16* qp = a.q + int64_t(qb + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
+#pragma unroll
+    for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
+  }
+  f32x16 o[G::kBlocks];
+#pragma unroll
+  for (int i = 0; i < G::kBlocks; ++i) o[i] = f32x16{};
+  float m = -1.0e30f;   // running max of this row, in log2 units
+  float lsum = 0.f;     // this lane's share of the row sum (other half: lane ^ 32)
+  V8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = T(1.f);
+
+  const int kb0 = r * G::kKPitch + 8 * h;
+  const VtBases vb = vt_operand_bases(lane);
+  // Half-step j covers kv tokens [32 j, 32 j + 32): K rows 32 (j % 2) ..
+  // of its tile's K buffer, V^T k-steps 2 (j % 2), 2 (j % 2) + 1. Lane
+  // (r, h) holds tokens 32 j + 8 (v / 4) + 4 h + v % 4 of row r.
+  auto half_scores = [&](int kbuf, int hh) {
+    const T* kt = sK + kbuf * G::kKHalves + kb0 + 32 * hh * G::kKPitch;
+    f32x16 s = mfma32(*reinterpret_cast<const V8*>(kt), qf[0], f32x16{});
+#pragma unroll
+    for (int st = 1; st < G::kSteps; ++st)
+      s = mfma32(*reinterpret_cast<const V8*>(kt + 16 * st), qf[st], s);
+    return s;
+  };
+  // Row max in log2 units (lanes r and r + 32 hold the two halves of row r).
+  auto row_max = [&](const f32x16& s) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
+    const auto sw = __builtin_amdgcn_permlane32_swap(f32_to_bits(mx), f32_to_bits(mx), false, false);
+    return fmaxf(bits_to_f32(sw[0]), bits_to_f32(sw[1])) * a.scale_log2;
+  };
+  // Lazy running max: moved only when a row's max exceeds it by more than
+  // 8 (log2 units), so probabilities stay <= 2^8 (exact in fp16), and the
+  // O rescale is skipped unless some row of the wave moved.
+  auto rescale = [&](float mx) {
+    if (__any(mx > m + 8.f)) {
+      const float m_new = mx > m + 8.f ? mx : m;
+      const float alpha = fast_exp2(m - m_new);
+      m = m_new;
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < G::kBlocks; ++dt) o[dt] *= alpha;
+    }
+  };
+  // P^T operands: k-step kk covers tokens 16 kk + 4 h + {0..3} and
+  // 16 kk + 8 + 4 h + {0..3}, i.e. score entries 8 kk + e. The row sum is
+  // taken over the rounded probabilities the P.V product uses.
+  auto probs = [&](const f32x16& s, V8 (&pb)[2]) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) pb[v >> 3][v & 7] = T(fast_exp2(fmaf(s[v], a.scale_log2, -m)));
+    lsum = dot8(pb[0], ones, lsum);
+    lsum = dot8(pb[1], ones, lsum);
+  };
+  auto pv = [&](int vbuf, int hh, const V8 (&pb)[2]) {
+    const T* vt = sVt + vbuf * G::kVtHalves;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int ks = 2 * hh + kk;
+#pragma unroll
+      for (int dt = 0; dt < G::kBlocks; ++dt) {
+        const V8 va = *reinterpret_cast<const V8*>(vt + vb.b[vt_operand_base_index(ks, dt)] +
+                                                    vt_operand_offset(dt));
+        o[dt] = mfma32(va, pb[kk], o[dt]);
+      }
+    }
+  };
+
+  // Interior tiles [t_first, t_int): before the workgroup's first row, in
+  // the KV range, no page id outside the pool (every wave runs them, rows
+  // past q_len on the first row's q).
+  const int t_int = any_bad ? t_first : max(t_first, min(ntiles, (prefix + q0 + 1) / kTileKV));
+  f32x16 sc;   // scores of the current half-step
+  // Pipelined step: V of the current half-step in V buffer vbuf (half hh),
+  // K of the next in K buffer kbuf_n (half hh_n).
+  auto step = [&](int kbuf_n, int hh_n, int vbuf, int hh) {
+    V8 pb[2];
+    const f32x16 sn = half_scores(kbuf_n, hh_n);
+    probs(sc, pb);
+    pv(vbuf, hh, pb);
+    const float mx = row_max(sn);
+    sc = sn;
+    rescale(mx);
+  };
+  auto step_last = [&](int vbuf, int hh) {
+    V8 pb[2];
+    probs(sc, pb);
+    pv(vbuf, hh, pb);
+  };
+  // One half-step with masks (diagonal tiles): causal, past the end of the
+  // row, and tokens on pages outside the pool.
+  const int j_last = wave_active ? min(wave_last_pos, kv_end - 1) >> 5 : -1;
+  const int lim0 = min(qpos + 1, kvl);   // a lane's tokens < lim0 are visible
+  auto half_masked = [&](int kbuf, int vbuf, int j) {
+    if (j > j_last) return;   // no visible key for this wave (uniform)
+    const int hh = j & 1;
+    f32x16 s = half_scores(kbuf, hh);
+    int lim = lim0 - 32 * j - 4 * h;   // entry 4 v4 + e is token 8 v4 + e past 32 j + 4 h
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      // The 4 tokens of a group share one page (page_size >= 4).
+      const int tok = 32 * j + 8 * v4 + 4 * h;
+      const bool skip = any_bad && tok < kv_end && bad_page(tok);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (skip || 8 * v4 + e >= lim) s[4 * v4 + e] = -INFINITY;
+    }
+    rescale(row_max(s));
+    V8 pb[2];
+    probs(s, pb);
+    pv(vbuf, hh, pb);
+  };
+
+  __syncthreads();   // tile t_first published
+  int kcur = 0, vcur = 0;
+  auto tile_end = [&]() {
+    kcur ^= 1;
+    vcur = vcur == 2 ? 0 : vcur + 1;
+  };
+  if (t_int > t_first) {
+    sc = half_scores(0, 0);
+    rescale(row_max(sc));
+    for (int it = t_first; it + 1 < t_int; ++it) {
+      step(kcur, 1, vcur, 0);
+      __syncthreads();
+      step(kcur ^ 1, 0, vcur, 1);
+      tile_end();
+    }
+    step(kcur, 1, vcur, 0);
+    __syncthreads();
+    step_last(vcur, 1);
+    tile_end();
+  }
+  for (int it = t_int; it < ntiles; ++it) {
+    half_masked(kcur, vcur, 2 * it);
+    half_masked(kcur, vcur, 2 * it + 1);
+    __syncthreads();
+    tile_end();
+  }
+
+  lsum += __shfl_xor(lsum, 32);
+  if (!row_ok) return;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  if (slot < 0) {
+    typedef typename Vec<T>::v4 V4;
+    f16* op = a.out + int64_t(qb + qrow) * a.o_tok + int64_t(hq) * a.o_head;
+#pragma unroll
+    for (int dt = 0; dt < G::kBlocks; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const V4 val = {T(o[dt][4 * g] * inv), T(o[dt][4 * g + 1] * inv),
+                        T(o[dt][4 * g + 2] * inv), T(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<V4*>(op + 32 * dt + 8 * g + 4 * h) = val;
+      }
+    return;
+  }
+  const int64_t prow = int64_t(slot) * G::kTileQ + (qrow - q0);
+  float* po = a.part_o + prow * D;
+#pragma unroll
+  for (int dt = 0; dt < G::kBlocks; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 val = {o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                         o[dt][4 * g + 3] * inv};
+      *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * g + 4 * h) = val;
+    }
+  if (h == 0) {
+    a.part_ml[2 * prow] = m;
+    a.part_ml[2 * prow + 1] = lsum;
+  }
+}
+
 // Combines the splits of one (sequence, q tile, q head): weight of split j
 // = 2^(m_j - max m) * sum_j, taken in split order.
 struct MergeArgs {
@@ -744,11 +1097,18 @@ __global__ __launch_bounds__(kRopeThreads) void rope_append_kernel(RopeArgs a) {
 template <typename T, int D>
 int run_prefill(const PrefillArgs& a, const MergeArgs& m, int num_tiles, int num_merge,
                 bool staged, hipStream_t s) {
-  constexpr int kThreads = Geom<D>::kThreads;
-  if (staged) {
-    paged_prefill_kernel<T, D, true><<<dim3(num_tiles), kThreads, 0, s>>>(a);
+  if constexpr (D <= 128) {
+    constexpr int kThreads = WsGeom<D>::kThreads;
+    if (staged)
+      paged_prefill_ws_kernel<T, D, true><<<dim3(num_tiles), kThreads, 0, s>>>(a);
+    else
+      paged_prefill_ws_kernel<T, D, false><<<dim3(num_tiles), kThreads, 0, s>>>(a);
   } else {
-    paged_prefill_kernel<T, D, false><<<dim3(num_tiles), kThreads, 0, s>>>(a);
+    constexpr int kThreads = Geom<D>::kThreads;
+    if (staged)
+      paged_prefill_kernel<T, D, true><<<dim3(num_tiles), kThreads, 0, s>>>(a);
+    else
+      paged_prefill_kernel<T, D, false><<<dim3(num_tiles), kThreads, 0, s>>>(a);
   }
   KSV_CHECK_LAUNCH();
   if (num_merge > 0) {
