@@ -562,6 +562,9 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
   __shared__ int s_bad[G::kWaves];
   __shared__ __attribute__((aligned(16))) T sK[2 * G::kKHalves];
   __shared__ __attribute__((aligned(16))) T sVt[3 * G::kVtHalves];
+  // Per K buffer, one byte per token of the tile: nonzero for a token with
+  // no data (on a page outside the pool, or past the end of the range).
+  __shared__ uint32_t s_inv[2][kTileKV / 4];
 
   const int32_t* item = a.tiles + kRec * blockIdx.x;
   const int seq = item[0];
@@ -591,81 +594,76 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
   const int t_first = kv_lo / kTileKV;
   const int pg_lo = kv_lo >> a.page_shift;
 
-  // Stage (or, for rows with too many pages, only scan) the page ids of
-  // [kv_lo, kv_end) and vote whether any is outside the pool.
-  bool any_bad = false;
-  {
-    const int npg = kv_end > kv_lo ? ((kv_end - 1) >> a.page_shift) + 1 - pg_lo : 0;
-    bool bad_id = false;
-    for (int i = threadIdx.x; i < npg; i += G::kThreads) {
-      const int p = pages[pg_lo + i];
-      const bool ok = p >= 0 && p < a.num_pages;
-      if constexpr (STAGED) s_pg[i] = ok ? p : -1;
-      bad_id |= !ok;
-    }
-    const bool wave_bad = __any(bad_id);
-    if (lane == 0) s_bad[wave] = wave_bad;
-    __syncthreads();
-    int bad = 0;
-#pragma unroll
-    for (int wv = 0; wv < G::kWaves; ++wv) bad |= s_bad[wv];
-    any_bad = __builtin_amdgcn_readfirstlane(bad) != 0;
-  }
-  auto bad_page = [&](int tok) {
-    const int p = STAGED ? s_pg[(tok >> a.page_shift) - pg_lo] : pages[tok >> a.page_shift];
-    return uint32_t(p) >= uint32_t(a.num_pages);
+  // Loader lanes: gather layout, tile registers, position lookups.
+  const int lw = wave - G::kComputeWaves;
+  const GatherLane gl = gather_lane<D>(D == 128 ? lw : lw % 2, lane);
+  const int ld_t = 16 * gl.g + 8 * gl.a + 4 * gl.h;
+  auto unit_v = [&](int u) { return D == 128 ? u == 0 : lw < 2; };
+  const f16* kbase = a.k + int64_t(hkv) * a.head_stride;
+  const f16* vbase = a.v + int64_t(hkv) * a.head_stride;
+  struct Regs {
+    V8 x[G::kUnits][4];
+    int nok;
   };
-
+  TileAt at;
+  auto read_ids = [&](int n0) {
+    const int tok = n0 + ld_t;
+    const int t = max(kv_lo, min(tok, kv_end - 1));   // clamped into the staged range
+    const int p = STAGED ? s_pg[(t >> a.page_shift) - pg_lo] : pages[t >> a.page_shift];
+    at = tile_at(p, tok, kv_end, a.num_pages, a.page_stride, a.token_stride, page_mask, 8 * gl.c);
+  };
+  auto read_ids_global = [&](int n0) {
+    const int tok = n0 + ld_t;
+    const int t = max(kv_lo, min(tok, kv_end - 1));
+    at = tile_at(pages[t >> a.page_shift], tok, kv_end, a.num_pages, a.page_stride, a.token_stride,
+                 page_mask, 8 * gl.c);
+  };
+  auto fetch = [&](Regs& rg) {
+#pragma unroll
+    for (int u = 0; u < G::kUnits; ++u) {
+      const f16* base = (unit_v(u) ? vbase : kbase) + at.off;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rg.x[u][i] = load_v8<T>(base + int64_t(i) * a.token_stride);
+    }
+    rg.nok = at.nok;
+  };
+  auto stash = [&](int kbuf, int vbuf, const Regs& rg) {
+#pragma unroll
+    for (int u = 0; u < G::kUnits; ++u) {
+      if (unit_v(u)) {
+#pragma unroll
+        for (int part = 0; part < 4; ++part)
+          vt_store<T>(sVt + vbuf * G::kVtHalves, gl, gl.c, rg.x[u], part, rg.nok);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<V8*>(&sK[kbuf * G::kKHalves + (ld_t + i) * G::kKPitch + 8 * gl.c]) =
+              rg.x[u][i];
+        // The K lanes of chunk 0 flag their 4 tokens (byte i: token i has no data).
+        if (gl.c == 0)
+          s_inv[kbuf][ld_t / 4] = rg.nok >= 4 ? 0u : 0x01010101u << (8 * rg.nok);
+      }
+    }
+  };
+  // Row block of a compute wave: waves w and w + 4 share a SIMD, and take
+  // blocks w and 7 - w, so that each SIMD pairs a short and a long run of
+  // diagonal half-steps (block b sees keys up to its own rows).
+  const int blk = wave < 4 ? wave : 11 - wave;
+  const int qrow = q0 + blk * 32 + r;
+  const bool row_ok = qrow < q_len;
+  const int npg = kv_end > kv_lo ? ((kv_end - 1) >> a.page_shift) + 1 - pg_lo : 0;
   if (loader) {
     // ---------------------------------------------------------- loader
-    const int lw = wave - G::kComputeWaves;
-    const GatherLane gl = gather_lane<D>(D == 128 ? lw : lw % 2, lane);
-    const int ld_t = 16 * gl.g + 8 * gl.a + 4 * gl.h;
-    auto unit_v = [&](int u) { return D == 128 ? u == 0 : lw < 2; };
-    const f16* kbase = a.k + int64_t(hkv) * a.head_stride;
-    const f16* vbase = a.v + int64_t(hkv) * a.head_stride;
-    struct Regs {
-      V8 x[G::kUnits][4];
-      int nok;
-    };
-    TileAt at;
-    auto read_ids = [&](int n0) {
-      const int tok = n0 + ld_t;
-      const int t = max(kv_lo, min(tok, kv_end - 1));   // clamped into the staged range
-      const int p = STAGED ? s_pg[(t >> a.page_shift) - pg_lo] : pages[t >> a.page_shift];
-      at = tile_at(p, tok, kv_end, a.num_pages, a.page_stride, a.token_stride, page_mask, 8 * gl.c);
-    };
-    auto fetch = [&](Regs& rg) {
-#pragma unroll
-      for (int u = 0; u < G::kUnits; ++u) {
-        const f16* base = (unit_v(u) ? vbase : kbase) + at.off;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) rg.x[u][i] = load_v8<T>(base + int64_t(i) * a.token_stride);
-      }
-      rg.nok = at.nok;
-    };
-    auto stash = [&](int kbuf, int vbuf, const Regs& rg) {
-#pragma unroll
-      for (int u = 0; u < G::kUnits; ++u) {
-        if (unit_v(u)) {
-#pragma unroll
-          for (int part = 0; part < 4; ++part)
-            vt_store<T>(sVt + vbuf * G::kVtHalves, gl, gl.c, rg.x[u], part, rg.nok);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<V8*>(&sK[kbuf * G::kKHalves + (ld_t + i) * G::kKPitch + 8 * gl.c]) =
-                rg.x[u][i];
-        }
-      }
-    };
     // Tile t_first + k is in register set k % 2 (ra even, rb odd). The
     // barrier after iteration u is barrier u - 1 of the compute waves.
+    // The first two tiles' loads go out while the compute waves stage the
+    // page ids, with their ids read from the table directly.
     Regs ra, rb;
-    read_ids(kv_lo);
+    read_ids_global(kv_lo);
     fetch(ra);
-    read_ids(kv_lo + kTileKV);
+    read_ids_global(kv_lo + kTileKV);
     fetch(rb);
+    __syncthreads();   // page ids staged
     stash(0, 0, ra);
     read_ids(kv_lo + 2 * kTileKV);
     fetch(ra);   // tile t_first + 2 (past the end: in-bounds reads, never stashed)
@@ -693,11 +691,25 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
   }
 
   // ------------------------------------------------------------ compute
-  const int qrow = q0 + wave * 32 + r;
-  const bool row_ok = qrow < q_len;
-  const int qpos = prefix + qrow;
-  const bool wave_active = q0 + wave * 32 < q_len;
-  const int wave_last_pos = prefix + min(q0 + wave * 32 + 31, q_len - 1);
+  // Stage (or, for rows with too many pages, only scan) the page ids of
+  // [kv_lo, kv_end) and vote whether any is outside the pool.
+  bool any_bad = false;
+  {
+    bool bad_id = false;
+    for (int i = threadIdx.x; i < npg; i += G::kComputeWaves * kWave) {
+      const int p = pages[pg_lo + i];
+      const bool ok = p >= 0 && p < a.num_pages;
+      if constexpr (STAGED) s_pg[i] = ok ? p : -1;
+      bad_id |= !ok;
+    }
+    const bool wave_bad = __any(bad_id);
+    if (lane == 0) s_bad[wave] = wave_bad;
+    __syncthreads();   // page ids staged
+    int bad = 0;
+#pragma unroll
+    for (int wv = 0; wv < G::kComputeWaves; ++wv) bad |= s_bad[wv];
+    any_bad = __builtin_amdgcn_readfirstlane(bad) != 0;
+  }
   // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8
   // (a row past q_len reads the sequence's first row and writes nothing).
   V8 qf[G::kSteps];
@@ -706,6 +718,7 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
   }
+  const int qpos = prefix + qrow;
   f32x16 o[G::kBlocks];
 #pragma unroll
   for (int i = 0; i < G::kBlocks; ++i) o[i] = f32x16{};
@@ -793,28 +806,36 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     probs(sc, pb);
     pv(vbuf, hh, pb);
   };
-  // One half-step with masks (diagonal tiles): causal, past the end of the
-  // row, and tokens on pages outside the pool.
-  const int j_last = wave_active ? min(wave_last_pos, kv_end - 1) >> 5 : -1;
-  const int lim0 = min(qpos + 1, kvl);   // a lane's tokens < lim0 are visible
-  auto half_masked = [&](int kbuf, int vbuf, int j) {
-    if (j > j_last) return;   // no visible key for this wave (uniform)
-    const int hh = j & 1;
-    f32x16 s = half_scores(kbuf, hh);
-    int lim = lim0 - 32 * j - 4 * h;   // entry 4 v4 + e is token 8 v4 + e past 32 j + 4 h
+  // Masks of half-step j's scores: causal and past the end of the row
+  // (tokens >= min(qpos + 1, kvl)), and with BAD tokens on pages outside
+  // the pool. Lane (r, h) entry 4 v4 + e is token 32 j + 8 v4 + e + 4 h.
+  const int lim0 = min(qpos + 1, kvl);
+  auto mask = [&](f32x16& sv, int j, int kbuf) {
+    // The bound is made opaque so that the compiler compares it with the
+    // 16 immediates instead of keeping 16 precomputed bounds live.
+    int lim = lim0 - 32 * j - 4 * h;
+    asm volatile("" : "+v"(lim));
 #pragma unroll
     for (int v4 = 0; v4 < 4; ++v4) {
-      // The 4 tokens of a group share one page (page_size >= 4).
-      const int tok = 32 * j + 8 * v4 + 4 * h;
-      const bool skip = any_bad && tok < kv_end && bad_page(tok);
+      // The loaders' flags of the group's 4 tokens.
+      const uint32_t inv = s_inv[kbuf][8 * (j & 1) + 2 * v4 + h];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (skip || 8 * v4 + e >= lim) s[4 * v4 + e] = -INFINITY;
+        if (((inv >> (8 * e)) & 1) || 8 * v4 + e >= lim) sv[4 * v4 + e] = -INFINITY;
     }
-    rescale(row_max(s));
+  };
+  // Diagonal tiles: a wave runs the half-steps up to its last visible key.
+  const bool wave_active = q0 + blk * 32 < q_len;
+  const int wave_last_pos = prefix + min(q0 + blk * 32 + 31, q_len - 1);
+  const int j_last = wave_active ? min(wave_last_pos, kv_end - 1) >> 5 : -1;
+  auto half_masked = [&](int kbuf, int vbuf, int j) {
+    if (j > j_last) return;   // uniform per wave
+    f32x16 sv = half_scores(kbuf, j & 1);
+    mask(sv, j, kbuf);
+    rescale(row_max(sv));
     V8 pb[2];
-    probs(s, pb);
-    pv(vbuf, hh, pb);
+    probs(sv, pb);
+    pv(vbuf, j & 1, pb);
   };
 
   __syncthreads();   // tile t_first published
@@ -823,6 +844,8 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     kcur ^= 1;
     vcur = vcur == 2 ? 0 : vcur + 1;
   };
+  // Interior tiles: every wave runs pipelined plain steps (rows past q_len
+  // on the first row's q).
   if (t_int > t_first) {
     sc = half_scores(0, 0);
     rescale(row_max(sc));
