@@ -559,6 +559,42 @@ def bench_prefill(args, device, page_size=16):
             "rope_append": rope}
 
 
+def mfma_ceiling(device, settle_s=0.5, reps=64):
+    """The rate this part sustains on the prefill kernels' 32x32x16 fp16
+    MFMA (kunserve_mfma_probe: two waves per SIMD of independent MFMAs on
+    every CU), with random N(0,1) operands and with constant ones. The
+    operands' bits set the power the matrix cores draw and so the clock the
+    part holds under its power limit; random operands draw what attention
+    operands draw. Each variant first runs for settle_s so that the clock
+    settles, then reps launches are timed."""
+    from kunserve_amd import _lib
+
+    wg = torch.cuda.get_device_properties(device).multi_processor_count
+    n = wg * 512 * 16
+    gen = torch.Generator(device=device)
+    gen.manual_seed(1008)
+    operands = {"constant": torch.full((n,), 0.01, dtype=torch.float16, device=device),
+                "random": torch.randn(n, generator=gen, device=device).half()}
+    sink = torch.empty(wg * 512, dtype=torch.float32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    iters = 1 << 14
+    flop = wg * 16 * iters * 32768
+    out = {"workgroups": wg, "flop_per_launch": flop}
+    for name, ops in operands.items():
+        def launch():
+            _lib.call("kunserve_mfma_probe", 0, ops.data_ptr(), sink.data_ptr(), wg, iters, stream)
+        t_end = time.perf_counter() + settle_s
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                launch()
+            torch.cuda.synchronize()
+        ms = region_ms(lambda: [launch() for _ in range(reps)], device) / reps
+        out[name + "_tflops"] = flop / (ms * 1e-3) / 1e12
+    log("fp16 MFMA ceiling (32x32x16, two waves per SIMD, every CU): constant operands "
+        "{constant_tflops:.0f}, random operands {random_tflops:.0f} TFLOP/s".format(**out))
+    return out
+
+
 # -------------------------------------------------------------------- swap
 
 
@@ -642,7 +678,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
     ap.add_argument("--only", choices=["decode", "prefill", "prefill256", "gqa", "bf16",
-                                       "bf16p256", "remap", "pmm", "swap"],
+                                       "bf16p256", "remap", "pmm", "swap", "mfma"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
@@ -665,6 +701,9 @@ def main():
 
     if args.only == "prefill":
         print(json.dumps({"prefill": bench_prefill(args, device)}))
+        return
+    if args.only == "mfma":
+        print(json.dumps({"mfma_ceiling": mfma_ceiling(device)}))
         return
     if args.only == "prefill256":
         print(json.dumps({"prefill_page256": bench_prefill(args, device, page_size=256)}))
@@ -703,10 +742,14 @@ def main():
     del dec["pool"], dec["qs"]
     torch.cuda.empty_cache()
     prefill = prefill256 = gqa = bf16 = bf16_256 = remap = pmm = swp = None
+    ceiling = None
     if args.only is None:
+        ceiling = mfma_ceiling(device)
         prefill = bench_prefill(args, device)
+        prefill["frac_of_random_operand_ceiling"] = prefill["tflops"] / ceiling["random_tflops"]
         torch.cuda.empty_cache()
         prefill256 = bench_prefill(args, device, page_size=256)
+        prefill256["frac_of_random_operand_ceiling"] = prefill256["tflops"] / ceiling["random_tflops"]
         torch.cuda.empty_cache()
         gqa = bench_gqa(args, device)
         torch.cuda.empty_cache()
@@ -755,6 +798,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "mfma_ceiling": ceiling,
         "prefill_page256": prefill256,
         "gqa_decode": gqa,
         "bf16_decode": bf16,

@@ -315,6 +315,19 @@ int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
                            void* workspace_dev, int64_t workspace_bytes,
                            kunserve_stream_t stream);
 
+/* MFMA calibration (no reference counterpart): each of num_workgroups
+ * workgroups runs 8 waves (two per SIMD) of `iterations` rounds of two
+ * independent 32x32x16 MFMAs (dtype KUNSERVE_DTYPE_F16 or _BF16) on
+ * per-lane operands read once from operands_dev (num_workgroups * 8192
+ * elements), and writes one float per thread to sink_dev (num_workgroups *
+ * 512 floats). One launch issues num_workgroups * 16 * iterations MFMAs of
+ * 32,768 flop. The benchmark times random and constant operands to give the
+ * prefill kernel's ceiling on the part it runs on: the operands' bits set
+ * the power the matrix cores draw, and so the clock the part holds. */
+int kunserve_mfma_probe(int32_t dtype, const void* operands_dev, float* sink_dev,
+                        int32_t num_workgroups, int32_t iterations,
+                        kunserve_stream_t stream);
+
 /* ------------------------------------------- fused page-id space (A6) */
 
 /* When N instances fuse into an N-stage pipeline (KunServe's balloon), each

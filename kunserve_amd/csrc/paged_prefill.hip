@@ -1539,3 +1539,58 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   return run_prefill_dim<f16>(pool->head_dim, a, m, info->num_tiles, info->num_merge,
                               pages_needed <= kMaxStagedPages, s);
 }
+
+// ------------------------------------------------------------ calibration
+// The rate this part sustains on the prefill kernels' MFMA: two waves per
+// SIMD issue independent 32x32x16 MFMAs on per-lane operands held in
+// registers. The operands' bits set the power the matrix cores draw, and so
+// the clock the part holds under its power limit: random operands draw what
+// attention operands draw, constant ones much less.
+namespace kunserve {
+namespace {
+
+constexpr int kMfmaProbeThreads = 512;
+
+template <typename T>
+__global__ __launch_bounds__(kMfmaProbeThreads) void mfma_probe_kernel(const T* operands, float* sink,
+                                                                       int iterations) {
+  typedef typename Vec<T>::v8 V8;
+  const int64_t t = int64_t(blockIdx.x) * kMfmaProbeThreads + threadIdx.x;
+  const V8 x = *reinterpret_cast<const V8*>(operands + 16 * t);
+  const V8 y = *reinterpret_cast<const V8*>(operands + 16 * t + 8);
+  f32x16 a0 = {}, a1 = {};
+  for (int i = 0; i < iterations; ++i) {
+    a0 = mfma32(x, y, a0);
+    a1 = mfma32(y, x, a1);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) s += a0[e] + a1[e];
+  sink[t] = s;
+}
+
+}  // namespace
+}  // namespace kunserve
+
+extern "C" int kunserve_mfma_probe(int32_t dtype, const void* operands_dev, float* sink_dev,
+                                   int32_t num_workgroups, int32_t iterations,
+                                   kunserve_stream_t stream) {
+  using namespace kunserve;
+  clear_error();
+  KSV_CHECK_ARG(dtype == KUNSERVE_DTYPE_F16 || dtype == KUNSERVE_DTYPE_BF16,
+                "dtype %d is not KUNSERVE_DTYPE_F16 or KUNSERVE_DTYPE_BF16", dtype);
+  KSV_CHECK_ARG(num_workgroups > 0 && iterations > 0,
+                "num_workgroups (%d) and iterations (%d) must be positive", num_workgroups,
+                iterations);
+  KSV_CHECK_ARG(operands_dev && sink_dev && aligned16(operands_dev) && aligned16(sink_dev),
+                "null or misaligned buffer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == KUNSERVE_DTYPE_BF16)
+    mfma_probe_kernel<bf16><<<num_workgroups, kMfmaProbeThreads, 0, s>>>(
+        static_cast<const bf16*>(operands_dev), sink_dev, iterations);
+  else
+    mfma_probe_kernel<f16><<<num_workgroups, kMfmaProbeThreads, 0, s>>>(
+        static_cast<const f16*>(operands_dev), sink_dev, iterations);
+  KSV_CHECK_LAUNCH();
+  return KUNSERVE_OK;
+}
