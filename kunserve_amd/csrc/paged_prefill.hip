@@ -844,9 +844,15 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     kcur ^= 1;
     vcur = vcur == 2 ? 0 : vcur + 1;
   };
-  // Interior tiles: every wave runs pipelined plain steps (rows past q_len
-  // on the first row's q).
-  if (t_int > t_first) {
+  // Interior tiles: every wave with a row before q_len runs pipelined plain
+  // steps (its rows past q_len on the first row's q).
+  if (!wave_active) {
+    // Every row of this wave is past q_len: only the barriers.
+    for (int it = t_first; it < t_int; ++it) {
+      __syncthreads();
+      tile_end();
+    }
+  } else if (t_int > t_first) {
     sc = half_scores(0, 0);
     rescale(row_max(sc));
     for (int it = t_first; it + 1 < t_int; ++it) {
