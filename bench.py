@@ -11,7 +11,10 @@ token once, plus q, out and page ids) with all inputs resident in HBM.
 Also measured: `prefill` — chunked-prefill attention with K/V append (16
 sequences, prompts U[512, 4096], prefixes U[0, 2048], chunk 512) as MFMA
 utilisation of the fp16 dense peak (and `prefill_page256`, the same
-workload on 256-token pages, the reference's default block size);
+workload on 256-token pages, the reference's default block size, and
+`bf16_prefill_page256` on a bf16 pool of 256-token pages, both reference
+defaults), beside `mfma_ceiling`, the rate the part sustains on fp16 MFMAs
+with random and with constant operands;
 `gqa_decode` — Llama-3-8B GQA decode (32/8 heads, batch 128, contexts
 U[1024, 8192]) as HBM bandwidth; `bf16_decode` — the headline decode on a
 bf16 pool (the reference's default dtype), and `bf16_decode_page256` on a
@@ -38,7 +41,7 @@ import numpy as np
 import torch
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
-FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 (and bf16) MFMA, TFLOP/s
 METRIC = "paged decode attn KV GB/s & % HBM peak at Llama-7B shape; prefill MFMA util"
 PROFILE_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
@@ -473,14 +476,15 @@ def cpu_baseline(res, budget_s: float) -> dict:
 # ----------------------------------------------------------------- prefill
 
 
-def bench_prefill(args, device, page_size=16):
+def bench_prefill(args, device, page_size=16, dtype=torch.float16):
     import kunserve_amd as ks
     from kunserve_amd import workloads
 
     w = workloads.chunked_prefill(page_size=page_size)
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed)
-    pool = ks.KVPool.allocate(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device)
+    pool = ks.KVPool.allocate(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device,
+                              dtype=dtype)
     fill_random_(pool.k, gen)
     fill_random_(pool.v, gen)
     steps = []
@@ -493,10 +497,10 @@ def bench_prefill(args, device, page_size=16):
         table = ks.PageTable(indptr, indices, kv, device)
         qi = torch.from_numpy(q_indptr).to(device)
         plan = ks.PrefillPlan(q_indptr, kv, w.num_qo_heads, w.num_kv_heads, device)
-        mk = lambda h: torch.randn((T, h, w.head_dim), generator=gen, device=device).half()
+        mk = lambda h: torch.randn((T, h, w.head_dim), generator=gen, device=device).to(dtype)
         steps.append((table, qi, plan, mk(w.num_qo_heads), mk(w.num_kv_heads),
                       mk(w.num_kv_heads), torch.empty((T, w.num_qo_heads, w.head_dim),
-                                                      dtype=torch.float16, device=device)))
+                                                      dtype=dtype, device=device)))
 
     def run(timer=None):
         for table, qi, plan, q, k, v, out in steps:
@@ -519,7 +523,7 @@ def bench_prefill(args, device, page_size=16):
             ks.rope_append_kv(pool, 0, table, qi, q, k, v, inv_freq)
 
     rope = None
-    if page_size == 16:
+    if page_size == 16 and dtype == torch.float16:
         run_rope()
         rope_reps = 4
         rope_ms = region_ms(lambda: [run_rope() for _ in range(rope_reps)], device) / rope_reps
@@ -550,10 +554,11 @@ def bench_prefill(args, device, page_size=16):
     log("prefill per-step attention ms: " + ", ".join(f"{t:.3f}" for t in per_step))
     flops = w.causal_flops()
     tflops = flops / (attn_ms * 1e-3) / 1e12
-    log(f"prefill (page {page_size}): {len(steps)} chunk steps, {elapsed * 1e3:.3f} ms with append; attention "
-        f"{attn_ms:.3f} ms = {tflops:.1f} TFLOP/s ({tflops / FP16_MFMA_PEAK_TFLOPS * 100:.1f}% "
-        f"of fp16 MFMA peak)")
-    return {"workload": w.name, "causal_tflop": flops / 1e12, "steps": len(steps),
+    name = "fp16" if dtype == torch.float16 else "bf16"
+    log(f"prefill ({name}, page {page_size}): {len(steps)} chunk steps, {elapsed * 1e3:.3f} ms with "
+        f"append; attention {attn_ms:.3f} ms = {tflops:.1f} TFLOP/s "
+        f"({tflops / FP16_MFMA_PEAK_TFLOPS * 100:.1f}% of the {name} MFMA peak)")
+    return {"workload": w.name, "dtype": name, "causal_tflop": flops / 1e12, "steps": len(steps),
             "ms_with_append": elapsed * 1e3, "attention_ms": attn_ms, "tflops": tflops,
             "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS, "page_size": page_size,
             "rope_append": rope}
@@ -678,7 +683,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
     ap.add_argument("--only", choices=["decode", "prefill", "prefill256", "gqa", "bf16",
-                                       "bf16p256", "remap", "pmm", "swap", "mfma"],
+                                       "bf16p256", "bf16prefill", "remap", "pmm", "swap",
+                                       "mfma"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
@@ -701,6 +707,10 @@ def main():
 
     if args.only == "prefill":
         print(json.dumps({"prefill": bench_prefill(args, device)}))
+        return
+    if args.only == "bf16prefill":
+        print(json.dumps({"bf16_prefill_page256": bench_prefill(args, device, page_size=256,
+                                                                dtype=torch.bfloat16)}))
         return
     if args.only == "mfma":
         print(json.dumps({"mfma_ceiling": mfma_ceiling(device)}))
@@ -741,7 +751,7 @@ def main():
     w = dec["workload"]
     del dec["pool"], dec["qs"]
     torch.cuda.empty_cache()
-    prefill = prefill256 = gqa = bf16 = bf16_256 = remap = pmm = swp = None
+    prefill = prefill256 = prefill_bf16 = gqa = bf16 = bf16_256 = remap = pmm = swp = None
     ceiling = None
     if args.only is None:
         ceiling = mfma_ceiling(device)
@@ -750,6 +760,8 @@ def main():
         torch.cuda.empty_cache()
         prefill256 = bench_prefill(args, device, page_size=256)
         prefill256["frac_of_random_operand_ceiling"] = prefill256["tflops"] / ceiling["random_tflops"]
+        torch.cuda.empty_cache()
+        prefill_bf16 = bench_prefill(args, device, page_size=256, dtype=torch.bfloat16)
         torch.cuda.empty_cache()
         gqa = bench_gqa(args, device)
         torch.cuda.empty_cache()
@@ -803,6 +815,7 @@ def main():
         "gqa_decode": gqa,
         "bf16_decode": bf16,
         "bf16_decode_page256": bf16_256,
+        "bf16_prefill_page256": prefill_bf16,
         "remap": remap,
         "pmm": pmm,
         "swap": swp,
