@@ -399,8 +399,9 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
     // Lazy running max: move it only when the tile's max exceeds it by more
-    // than 8 (log2 units). Probabilities then stay <= 2^8 (exact in fp16 and
-    // fp32), and the O rescale is skipped unless some row of the wave moved.
+    // than 8 (log2 units). Probabilities then stay <= 2^8, far inside the
+    // fp16 range, and the O rescale is skipped unless some row of the wave
+    // moved.
     if (__any(mx > m + 8.f)) {
       const float m_new = mx > m + 8.f ? mx : m;
       const float alpha = fast_exp2(m - m_new);
@@ -526,15 +527,17 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
 // Warp-specialised variant for head_dim 64 and 128. A workgroup is 12
 // waves: compute waves 0-7 (32 query rows each, two per SIMD) only read
 // LDS and run the math; loader waves 8-11 (one per SIMD) only gather K/V
-// tiles from the pages into LDS. Loaders run one tile ahead: tile u is
-// written between barriers u - 2 and u - 1, into K buffer u % 2 and V
-// buffer u % 3, from registers loaded two tiles earlier. Compute waves run
-// barrier t between the two 32-token halves of tile t (the second half's
-// score MFMAs read K of tile t + 1, published by that barrier). The
-// interior tiles, whose keys every row sees, run a straight-line pipeline
-// (the scores of half-step j + 1 issue between the exponentials of j, and
-// the P.V of j beside the max of j + 1); the diagonal tiles run each half
-// on its own, with the causal / past-the-end / bad-page masks.
+// tiles from the pages into LDS. Loaders run one tile ahead: with tiles
+// counted from the item's first, tile u is written between barriers u - 2
+// and u - 1, into K buffer u % 2 and V buffer u % 3, from registers loaded
+// two tiles earlier. Compute waves run barrier t between the two 32-token
+// halves of tile t (the second half's score MFMAs read K of tile t + 1,
+// published by that barrier). The interior tiles, whose keys every row
+// sees, run a straight-line pipeline (the scores of half-step j + 1 issue
+// between the exponentials of j, and the P.V of j beside the max of j + 1);
+// the diagonal tiles run each half on its own, with the causal /
+// past-the-end / no-data masks. Waves with no row before q_len only pass
+// the barriers.
 template <int D>
 struct WsGeom {
   static_assert(D == 64 || D == 128, "warp-specialised prefill is for head_dim 64 and 128");
@@ -750,8 +753,8 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     return fmaxf(bits_to_f32(sw[0]), bits_to_f32(sw[1])) * a.scale_log2;
   };
   // Lazy running max: moved only when a row's max exceeds it by more than
-  // 8 (log2 units), so probabilities stay <= 2^8 (exact in fp16), and the
-  // O rescale is skipped unless some row of the wave moved.
+  // 8 (log2 units), so probabilities stay <= 2^8 (far inside the fp16
+  // range), and the O rescale is skipped unless some row of the wave moved.
   auto rescale = [&](float mx) {
     if (__any(mx > m + 8.f)) {
       const float m_new = mx > m + 8.f ? mx : m;
@@ -786,8 +789,7 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
   };
 
   // Interior tiles [t_first, t_int): before the workgroup's first row, in
-  // the KV range, no page id outside the pool (every wave runs them, rows
-  // past q_len on the first row's q).
+  // the KV range, no page id outside the pool.
   const int t_int = any_bad ? t_first : max(t_first, min(ntiles, (prefix + q0 + 1) / kTileKV));
   f32x16 sc;   // scores of the current half-step
   // Pipelined step: V of the current half-step in V buffer vbuf (half hh),
@@ -807,8 +809,8 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     pv(vbuf, hh, pb);
   };
   // Masks of half-step j's scores: causal and past the end of the row
-  // (tokens >= min(qpos + 1, kvl)), and with BAD tokens on pages outside
-  // the pool. Lane (r, h) entry 4 v4 + e is token 32 j + 8 v4 + e + 4 h.
+  // (tokens >= min(qpos + 1, kvl)), and tokens the loaders flagged as having
+  // no data. Lane (r, h) entry 4 v4 + e is token 32 j + 8 v4 + e + 4 h.
   const int lim0 = min(qpos + 1, kvl);
   auto mask = [&](f32x16& sv, int j, int kbuf) {
     // The bound is made opaque so that the compiler compares it with the
