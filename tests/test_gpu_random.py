@@ -62,6 +62,22 @@ def test_decode_random_cases(device, hkv, ratio, d, ps, kv, part, bf16, seed):
                      max_size=4),
        bf16=st.booleans(), seed=st.integers(0, 2**16))
 def test_prefill_random_cases(device, hkv, ratio, d, ps, rows, bf16, seed):
+    _check_prefill(device, hkv, ratio, d, ps, rows, bf16, seed)
+
+
+@settings(RANDOM, max_examples=40)
+@given(hkv=st.sampled_from([1, 2, 4]), ratio=st.sampled_from([1, 2, 4]),
+       d=st.sampled_from([64, 128, 256]), ps=st.sampled_from([4, 16, 64, 256]),
+       rows=st.lists(st.tuples(st.integers(1, 1600), st.integers(0, 3000)), min_size=1,
+                     max_size=3),
+       bf16=st.booleans(), seed=st.integers(0, 2**16))
+def test_prefill_random_long_rows(device, hkv, ratio, d, ps, rows, bf16, seed):
+    """Rows of several q tiles, diagonal tiles deep into long prefixes, and
+    steps small enough that the plan splits the KV range."""
+    _check_prefill(device, hkv, ratio, d, ps, rows, bf16, seed)
+
+
+def _check_prefill(device, hkv, ratio, d, ps, rows, bf16, seed):
     dtype = torch.bfloat16 if bf16 else torch.float16
     rng = np.random.default_rng(seed)
     q_lens = np.array([r[0] for r in rows], dtype=np.int32)
