@@ -555,13 +555,30 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16):
     flops = w.causal_flops()
     tflops = flops / (attn_ms * 1e-3) / 1e12
     name = "fp16" if dtype == torch.float16 else "bf16"
+    # Algorithmic bytes of the pass: each step reads every row's K and V
+    # once per KV head, its q and its page ids, and writes its out. Against
+    # them, the arithmetic intensity and the roofline time (the larger of
+    # the MFMA-bound and HBM-bound times at the peaks).
+    elem = 2
+    nbytes = 0
+    for rows, ql, kv in w.steps():
+        T = int(ql.sum())
+        nbytes += int(kv.sum()) * w.num_kv_heads * w.head_dim * 2 * elem
+        nbytes += 2 * T * w.num_qo_heads * w.head_dim * elem
+        nbytes += int(((kv + w.page_size - 1) // w.page_size).sum()) * 4
+    roof_ms = max(flops / (FP16_MFMA_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
     log(f"prefill ({name}, page {page_size}): {len(steps)} chunk steps, {elapsed * 1e3:.3f} ms with "
         f"append; attention {attn_ms:.3f} ms = {tflops:.1f} TFLOP/s "
         f"({tflops / FP16_MFMA_PEAK_TFLOPS * 100:.1f}% of the {name} MFMA peak)")
+    log(f"prefill ({name}, page {page_size}): {nbytes / 1e9:.2f} GB algorithmic, "
+        f"{flops / nbytes:.0f} flop/B against a ridge of "
+        f"{FP16_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):.0f}; roofline time "
+        f"{roof_ms:.3f} ms = {roof_ms / attn_ms * 100:.1f}% of the measured")
     return {"workload": w.name, "dtype": name, "causal_tflop": flops / 1e12, "steps": len(steps),
             "ms_with_append": elapsed * 1e3, "attention_ms": attn_ms, "tflops": tflops,
             "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS, "page_size": page_size,
-            "rope_append": rope}
+            "algorithmic_bytes": nbytes, "flop_per_byte": flops / nbytes,
+            "roofline_ms": roof_ms, "roofline_frac": roof_ms / attn_ms, "rope_append": rope}
 
 
 def mfma_ceiling(device, settle_s=0.5, reps=64):
