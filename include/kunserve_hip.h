@@ -93,7 +93,11 @@ typedef struct {
 
 /* ---------------------------------------------------------------- misc */
 
-/* Library ABI version (major*100 + minor). */
+/* Library ABI version (major*100 + minor): 300. Major 2 gave
+ * kunserve_prefill_plan_bound and kunserve_prefill_plan a head_dim argument
+ * and kunserve_prefill_plan_info its head_dim field; major 3 gave
+ * kunserve_paged_decode(_noalloc) the q_token_dev argument and
+ * kunserve_paged_prefill the q_start_dev argument (mixed steps in place). */
 int32_t kunserve_version(void);
 
 /* Message of the last error raised on the calling thread ("" if none). */
@@ -223,13 +227,17 @@ int64_t kunserve_decode_workspace_bytes(const kunserve_decode_plan_info* info,
                                         int32_t num_qo_heads,
                                         int32_t head_dim);
 
-/* o[b, h, :] = softmax(q[b, h, :] . K[b, g(h)]^T * sm_scale) . V[b, g(h)]
+/* o[t, h, :] = softmax(q[t, h, :] . K[b, g(h)]^T * sm_scale) . V[b, g(h)]
  * over the kv_len[b] tokens of sequence b in layer `layer`, with
- * g(h) = h / (num_qo_heads / num_kv_heads). q and out are
- * [num_seqs, num_qo_heads, head_dim] of the pool dtype (fp16 or bf16);
- * fp32 accumulation. */
+ * g(h) = h / (num_qo_heads / num_kv_heads) and t = q_token[b], or t = b
+ * when q_token_dev is NULL. q and out are [num_tokens, num_qo_heads,
+ * head_dim] of the pool dtype (fp16 or bf16); fp32 accumulation. q_token
+ * (device int32 [num_seqs]) lets the decode rows of a mixed step
+ * (kunserve/flash_backend.py:1870-1950, rows of request.py:654-670) read q
+ * and write out in place, among the step's prefill tokens. */
 int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer,
                           const kunserve_page_table* table,
+                          const int32_t* q_token_dev,
                           const kunserve_tensor3* q, kunserve_tensor3* out,
                           int32_t num_qo_heads, float sm_scale,
                           const int32_t* plan_dev,
@@ -250,6 +258,7 @@ int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer,
 int64_t kunserve_paged_decode_noalloc_max_bytes(void);
 int kunserve_paged_decode_noalloc(const kunserve_kv_pool* pool, int32_t layer,
                                   const kunserve_page_table* table,
+                                  const int32_t* q_token_dev,
                                   const kunserve_tensor3* q, kunserve_tensor3* out,
                                   int32_t num_qo_heads, float sm_scale,
                                   const int32_t* plan_dev,
@@ -301,13 +310,19 @@ int64_t kunserve_prefill_workspace_bytes(const kunserve_prefill_plan_info* info)
 /* Causal attention of the q_len[b] new rows of each sequence against its
  * kv_len[b] cached tokens (new ones already appended): q row i of
  * sequence b sees positions [0, kv_len[b] - q_len[b] + i]. q and out are
- * [num_tokens, num_qo_heads, head_dim] of the pool dtype with rows grouped
- * by q_indptr. fp16 or bf16 MFMA for Q.K^T and P.V, fp32 accumulation and
- * softmax. head_dim 64, 128 or 256 (KUNSERVE_EUNSUPPORTED otherwise); the
- * plan must have been made for the pool's head_dim. */
+ * [num_tokens, num_qo_heads, head_dim] of the pool dtype; row i of
+ * sequence b is token q_start[b] + i, or q_indptr[b] + i when q_start_dev
+ * is NULL (q_len[b] = q_indptr[b+1] - q_indptr[b] either way). q_start
+ * (device int32 [num_seqs]) lets the prefill rows of a mixed step
+ * (kunserve/flash_backend.py:1870-1950) read q and write out in place,
+ * among the step's decode tokens. fp16 or bf16 MFMA for Q.K^T and P.V,
+ * fp32 accumulation and softmax. head_dim 64, 128 or 256
+ * (KUNSERVE_EUNSUPPORTED otherwise); the plan must have been made for the
+ * pool's head_dim. */
 int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
                            const kunserve_page_table* table,
                            const int32_t* q_indptr_dev,
+                           const int32_t* q_start_dev,
                            const kunserve_tensor3* q, kunserve_tensor3* out,
                            int32_t num_qo_heads, float sm_scale,
                            const int32_t* plan_dev,

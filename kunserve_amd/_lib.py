@@ -83,13 +83,14 @@ SIGNATURES = {
     "kunserve_decode_plan": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
                                      c_void_p, c_int64, POINTER(DecodePlanInfo)]),
     "kunserve_decode_workspace_bytes": (c_int64, [POINTER(DecodePlanInfo), c_int32, c_int32]),
-    "kunserve_paged_decode": (c_int, [POINTER(KVPool), c_int32, POINTER(PageTable),
+    "kunserve_paged_decode": (c_int, [POINTER(KVPool), c_int32, POINTER(PageTable), c_void_p,
                                       POINTER(Tensor3), POINTER(Tensor3), c_int32, c_float,
                                       c_void_p, POINTER(DecodePlanInfo), c_void_p, c_int64,
                                       c_void_p]),
     "kunserve_paged_decode_noalloc_max_bytes": (c_int64, []),
     "kunserve_paged_decode_noalloc": (c_int, [POINTER(KVPool), c_int32, POINTER(PageTable),
-                                              POINTER(Tensor3), POINTER(Tensor3), c_int32,
+                                              c_void_p, POINTER(Tensor3), POINTER(Tensor3),
+                                              c_int32,
                                               c_float, c_void_p, POINTER(DecodePlanInfo),
                                               c_void_p]),
     "kunserve_prefill_plan_bound": (c_int64, [c_void_p, c_int32, c_int32, c_int32]),
@@ -97,7 +98,7 @@ SIGNATURES = {
                                       c_int32, c_void_p, c_int64, POINTER(PrefillPlanInfo)]),
     "kunserve_prefill_workspace_bytes": (c_int64, [POINTER(PrefillPlanInfo)]),
     "kunserve_paged_prefill": (c_int, [POINTER(KVPool), c_int32, POINTER(PageTable), c_void_p,
-                                       POINTER(Tensor3), POINTER(Tensor3), c_int32, c_float,
+                                       c_void_p, POINTER(Tensor3), POINTER(Tensor3), c_int32, c_float,
                                        c_void_p, POINTER(PrefillPlanInfo), c_void_p, c_int64,
                                        c_void_p]),
     "kunserve_fused_pool": (c_int, [POINTER(KVPool), c_int64, c_int32, POINTER(KVPool)]),

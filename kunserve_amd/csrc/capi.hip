@@ -48,7 +48,7 @@ int check_pool(const kunserve_kv_pool* p, bool need_vec_align) {
 
 }  // namespace kunserve
 
-extern "C" int32_t kunserve_version(void) { return 100; }
+extern "C" int32_t kunserve_version(void) { return 300; }
 
 extern "C" const char* kunserve_last_error(void) { return kunserve::g_last_error.c_str(); }
 

@@ -45,6 +45,7 @@ constexpr float kNegBig = -1.0e30f;      // finite "minus infinity" for running 
 __device__ __attribute__((aligned(16))) f16 g_zero_row[256];
 
 struct DecodeArgs {
+  const int32_t* q_token;   // null, or [num_seqs]: token of q and out of each sequence
   const f16* q;
   int64_t q_tok, q_head;
   f16* out;
@@ -105,6 +106,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
   if (!decode_work(a, item, hg)) return;   // padding workgroup (uniform: no barrier reached)
   const int32_t* w = a.work + 4 * item;
   const int seq = w[0], tb = w[1], te = w[2], slot = w[3];
+  const int tok = a.q_token ? a.q_token[seq] : seq;   // q / out token of the sequence
   const int hq0 = hg * G;
   const int hkv = hq0 / a.ratio;
   const int page_mask = (1 << a.page_shift) - 1;
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
   V8 qv[G];
 #pragma unroll
   for (int g = 0; g < G; ++g)
-    qv[g] = load_v8<T>(a.q + int64_t(seq) * a.q_tok + int64_t(hq0 + g) * a.q_head + col * 8);
+    qv[g] = load_v8<T>(a.q + int64_t(tok) * a.q_tok + int64_t(hq0 + g) * a.q_head + col * 8);
 
   float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -262,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
     const float r = lsum > 0.f ? o / lsum : 0.f;
     const int hq = hq0 + g;
     if (slot < 0) {
-      reinterpret_cast<T*>(a.out)[int64_t(seq) * a.o_tok + int64_t(hq) * a.o_head + d] = T(r);
+      reinterpret_cast<T*>(a.out)[int64_t(tok) * a.o_tok + int64_t(hq) * a.o_head + d] = T(r);
     } else {
       a.part_o[(int64_t(slot) * a.num_qo_heads + hq) * D + d] = r;
       if (d == 0)
@@ -319,6 +321,7 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   if (!decode_work(a, item, hg)) return;   // padding workgroup (uniform: no barrier reached)
   const int32_t* w = a.work + 4 * item;
   const int seq = w[0], tb = w[1], te = w[2], slot = w[3];
+  const int tok = a.q_token ? a.q_token[seq] : seq;   // q / out token of the sequence
   const int hq0 = hg * G;
   const int hkv = hq0 / a.ratio;
   const int page_mask = (1 << a.page_shift) - 1;
@@ -342,7 +345,7 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   V8 qb[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s)
-    qb[s] = j < G ? load_v8<T>(a.q + int64_t(seq) * a.q_tok + int64_t(hq0 + j) * a.q_head +
+    qb[s] = j < G ? load_v8<T>(a.q + int64_t(tok) * a.q_tok + int64_t(hq0 + j) * a.q_head +
                                32 * s + 8 * tg)
                   : V8{};
   f32x4 o[8];
@@ -506,7 +509,7 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
     const float r = ls > 0.f ? acc / ls : 0.f;
     const int hq = hq0 + g;
     if (slot < 0) {
-      reinterpret_cast<T*>(a.out)[int64_t(seq) * a.o_tok + int64_t(hq) * a.o_head + d] = T(r);
+      reinterpret_cast<T*>(a.out)[int64_t(tok) * a.o_tok + int64_t(hq) * a.o_head + d] = T(r);
     } else {
       a.part_o[(int64_t(slot) * a.num_qo_heads + hq) * D + d] = r;
       if (d == 0)
@@ -521,6 +524,7 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
 // dimensions over the partitions.
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merges,
+                                                             const int32_t* q_token,
                                                              const float* part_o,
                                                              const float* part_lse, T* out,
                                                              int64_t o_tok, int64_t o_head,
@@ -556,7 +560,8 @@ __global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merg
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) wsum += __shfl_xor(wsum, off);
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  T* dst = out + int64_t(seq) * o_tok + int64_t(hq) * o_head + lane * DPL;
+  const int tok = q_token ? q_token[seq] : seq;
+  T* dst = out + int64_t(tok) * o_tok + int64_t(hq) * o_head + lane * DPL;
 #pragma unroll
   for (int e = 0; e < DPL; ++e) dst[e] = T(o[e] * inv);
 }
@@ -595,10 +600,11 @@ int launch_decode(const DecodeArgs& a, int group, dim3 grid, hipStream_t s) {
 }
 
 template <typename T, int D>
-int launch_merge(const int32_t* merges, int num_merge, const float* po, const float* pl, f16* out,
-                 int64_t o_tok, int64_t o_head, int hq, hipStream_t s) {
+int launch_merge(const int32_t* merges, int num_merge, const int32_t* q_token, const float* po,
+                 const float* pl, f16* out, int64_t o_tok, int64_t o_head, int hq, hipStream_t s) {
   dim3 grid(num_merge, hq);
-  decode_merge_kernel<T, D><<<grid, kWave, 0, s>>>(merges, po, pl, reinterpret_cast<T*>(out),
+  decode_merge_kernel<T, D><<<grid, kWave, 0, s>>>(merges, q_token, po, pl,
+                                                   reinterpret_cast<T*>(out),
                                                    o_tok, o_head, hq);
   KSV_CHECK_LAUNCH();
   return KUNSERVE_OK;
@@ -619,13 +625,13 @@ int run_decode(const DecodeArgs& a, const kunserve_decode_plan_info& info, const
   const int32_t* merges = plan_dev + 4 * int64_t(info.num_work);
   switch (head_dim) {
     case 64:
-      return launch_merge<T, 64>(merges, info.num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
+      return launch_merge<T, 64>(merges, info.num_merge, a.q_token, a.part_o, a.part_lse, a.out, a.o_tok,
                                  a.o_head, num_qo_heads, s);
     case 128:
-      return launch_merge<T, 128>(merges, info.num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
+      return launch_merge<T, 128>(merges, info.num_merge, a.q_token, a.part_o, a.part_lse, a.out, a.o_tok,
                                   a.o_head, num_qo_heads, s);
     default:
-      return launch_merge<T, 256>(merges, info.num_merge, a.part_o, a.part_lse, a.out, a.o_tok,
+      return launch_merge<T, 256>(merges, info.num_merge, a.q_token, a.part_o, a.part_lse, a.out, a.o_tok,
                                   a.o_head, num_qo_heads, s);
   }
 }
@@ -727,6 +733,7 @@ extern "C" int64_t kunserve_decode_workspace_bytes(const kunserve_decode_plan_in
 
 extern "C" int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer,
                                      const kunserve_page_table* table,
+                                     const int32_t* q_token_dev,
                                      const kunserve_tensor3* q, kunserve_tensor3* out,
                                      int32_t num_qo_heads, float sm_scale,
                                      const int32_t* plan_dev,
@@ -758,6 +765,7 @@ extern "C" int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer
     return KUNSERVE_ENOSPC;
   }
   DecodeArgs a{};
+  a.q_token = q_token_dev;
   a.q = static_cast<const f16*>(q->data);
   a.q_tok = q->token_stride;
   a.q_head = q->head_stride;
@@ -844,6 +852,7 @@ extern "C" int64_t kunserve_paged_decode_noalloc_max_bytes(void) {
 
 extern "C" int kunserve_paged_decode_noalloc(const kunserve_kv_pool* pool, int32_t layer,
                                              const kunserve_page_table* table,
+                                             const int32_t* q_token_dev,
                                              const kunserve_tensor3* q, kunserve_tensor3* out,
                                              int32_t num_qo_heads, float sm_scale,
                                              const int32_t* plan_dev,
@@ -873,6 +882,6 @@ extern "C" int kunserve_paged_decode_noalloc(const kunserve_kv_pool* pool, int32
     rc = scratch_address(device, &ws);
     if (rc) return rc;
   }
-  return kunserve_paged_decode(pool, layer, table, q, out, num_qo_heads, sm_scale, plan_dev, info,
-                               ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
+  return kunserve_paged_decode(pool, layer, table, q_token_dev, q, out, num_qo_heads, sm_scale,
+                               plan_dev, info, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
 }

@@ -82,6 +82,7 @@ struct PrefillArgs {
   const int32_t* indices;
   const int32_t* kv_len;
   const int32_t* q_indptr;
+  const int32_t* q_start; // null, or [num_seqs]: first token of each row in q and out
   const int32_t* tiles;   // [num_tiles][kRec]: see kRec
   float* part_o;          // [slots][tile_q][head_dim] split partials, normalised
   float* part_ml;         // [slots][tile_q][2] running max (log2 units), sum
@@ -233,6 +234,7 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   const int hkv = hq / a.ratio;
   const int qb = a.q_indptr[seq];
   const int q_len = a.q_indptr[seq + 1] - qb;
+  const int qt = a.q_start ? a.q_start[seq] : qb;   // the row's first token of q and out
   const int kvl = a.kv_len[seq];
   const int prefix = kvl - q_len;
   const int32_t* pages = a.indices + a.indptr[seq];
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   // writes no output).
   V8 qf[G::kSteps];
   {
-    const f16* qp = a.q + int64_t(qb + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
+    const f16* qp = a.q + int64_t(qt + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
   }
@@ -495,7 +497,7 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   if (!row_ok) return;
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   if (slot < 0) {
-    f16* op = a.out + int64_t(qb + qrow) * a.o_tok + int64_t(hq) * a.o_head;
+    f16* op = a.out + int64_t(qt + qrow) * a.o_tok + int64_t(hq) * a.o_head;
 #pragma unroll
     for (int dt = 0; dt < G::kBlocks; ++dt)
 #pragma unroll
@@ -588,6 +590,7 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
   const int hkv = hq / a.ratio;
   const int qb = a.q_indptr[seq];
   const int q_len = a.q_indptr[seq + 1] - qb;
+  const int qt = a.q_start ? a.q_start[seq] : qb;   // the row's first token of q and out
   const int kvl = a.kv_len[seq];
   const int prefix = kvl - q_len;
   const int32_t* pages = a.indices + a.indptr[seq];
@@ -717,7 +720,7 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
   // (a row past q_len reads the sequence's first row and writes nothing).
   V8 qf[G::kSteps];
   {
-    const f16* qp = a.q + int64_t(qb + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
+    const f16* qp = a.q + int64_t(qt + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
   }
@@ -880,7 +883,7 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   if (slot < 0) {
     typedef typename Vec<T>::v4 V4;
-    f16* op = a.out + int64_t(qb + qrow) * a.o_tok + int64_t(hq) * a.o_head;
+    f16* op = a.out + int64_t(qt + qrow) * a.o_tok + int64_t(hq) * a.o_head;
 #pragma unroll
     for (int dt = 0; dt < G::kBlocks; ++dt)
 #pragma unroll
@@ -914,6 +917,7 @@ struct MergeArgs {
   const float* part_o;
   const float* part_ml;
   const int32_t* q_indptr;
+  const int32_t* q_start;  // as PrefillArgs::q_start
   f16* out;
   int64_t o_tok, o_head;
 };
@@ -929,6 +933,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MergeArgs a) {
   const int seq = rec[0], q0 = rec[1], hq = rec[2], s0 = rec[3], n = rec[4];
   const int qb = a.q_indptr[seq];
   const int q_len = a.q_indptr[seq + 1] - qb;
+  const int qt = a.q_start ? a.q_start[seq] : qb;   // the row's first token of q and out
   {
     const int row = blockIdx.y * merge_rows(D) + int(threadIdx.x) / (D / 8);
     const int c = int(threadIdx.x) % (D / 8);
@@ -954,7 +959,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MergeArgs a) {
       }
     }
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-    f16* op = a.out + int64_t(qb + q0 + row) * a.o_tok + int64_t(hq) * a.o_head + 8 * c;
+    f16* op = a.out + int64_t(qt + q0 + row) * a.o_tok + int64_t(hq) * a.o_head + 8 * c;
     *reinterpret_cast<V4*>(op) = {T(acc[0] * inv), T(acc[1] * inv), T(acc[2] * inv),
                                   T(acc[3] * inv)};
     *reinterpret_cast<V4*>(op + 4) = {T(acc[4] * inv), T(acc[5] * inv), T(acc[6] * inv),
@@ -1458,7 +1463,8 @@ extern "C" int64_t kunserve_prefill_workspace_bytes(const kunserve_prefill_plan_
 
 extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t layer,
                                       const kunserve_page_table* table,
-                                      const int32_t* q_indptr_dev, const kunserve_tensor3* q,
+                                      const int32_t* q_indptr_dev, const int32_t* q_start_dev,
+                                      const kunserve_tensor3* q,
                                       kunserve_tensor3* out, int32_t num_qo_heads,
                                       float sm_scale, const int32_t* plan_dev,
                                       const kunserve_prefill_plan_info* info,
@@ -1525,6 +1531,7 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   a.indices = table->indices_dev;
   a.kv_len = table->kv_len_dev;
   a.q_indptr = q_indptr_dev;
+  a.q_start = q_start_dev;
   a.tiles = plan_dev;
   a.part_o = static_cast<float*>(workspace_dev);
   a.part_ml = a.part_o ? a.part_o + int64_t(info->num_slots) * info->tile_q * pool->head_dim
@@ -1537,6 +1544,7 @@ extern "C" int kunserve_paged_prefill(const kunserve_kv_pool* pool, int32_t laye
   m.part_o = a.part_o;
   m.part_ml = a.part_ml;
   m.q_indptr = q_indptr_dev;
+  m.q_start = q_start_dev;
   m.out = a.out;
   m.o_tok = a.o_tok;
   m.o_head = a.o_head;

@@ -207,9 +207,13 @@ class LlamaOp:
         pool, so no request may hold them. The memory comes back holding KV
         data: the weights themselves are reloaded by the caller (the
         reference pulls them from a peer instance over NCCL,
-        kunserve/llm_engine.py:553-558)."""
+        kunserve/llm_engine.py:553-558). The op leaves its balloon group:
+        page ids are unfused again (restore_from_fusion resets the fusion
+        size, kunserve/block_manager.py:347-348). Without max_extend_pages
+        nothing was dropped and [] is returned."""
+        self.fusion_size = 1
         if self.pmm is None:
-            raise RuntimeError("LlamaOp was built without max_extend_pages")
+            return []
         by_segment = {sid: layer for layer, sid in self._weight_segments.items()}
         restored = []
         while self.pmm.dropped:

@@ -158,7 +158,9 @@ def fused_page_ids(ids, base_pages: int, fusion_size: int, num_fused_pages: int)
 
 def kv_lens_for_step(first_token_indexes: Sequence[int], q_lens: Sequence[int],
                      is_prefill_requests: Sequence[int], use_tensor_cores: bool = False,
-                     is_context_stage: Optional[Sequence[int]] = None) -> np.ndarray:
+                     is_context_stage: Optional[Sequence[int]] = None,
+                     pages_per_row: Optional[Sequence[int]] = None,
+                     page_size: int = 0) -> np.ndarray:
     """KV length of each row after this step's tokens are appended.
 
     kunserve/request.py:447-462: a prefill row's first index is
@@ -172,20 +174,22 @@ def kv_lens_for_step(first_token_indexes: Sequence[int], q_lens: Sequence[int],
     With use_tensor_cores every row arrives flagged as prefill
     (kunserve/request.py:667-670, kunserve/flash_backend.py:2460-2462), so
     the flag no longer tells a decode row from a one-token prefill chunk.
-    Rows with one input token and a first index > 0 are then taken as decode
-    rows (kv_len = first), which keeps every append inside the blocks the
-    block manager allocated; a one-token row at first index 0 can only be
-    the first chunk of a one-token prompt (kv_len = 1). A one-token prefill
-    chunk at first index > 0 (the last chunk of a prompt one token longer
-    than a chunk multiple) is the case these arguments cannot separate: the
-    caller passes the rows' real stages as is_context_stage
-    ([int(r.is_context_stage()) for r in requests]), which then decides for
-    every row instead of the flags.
+    The caller then passes the rows' real stages as is_context_stage
+    ([int(r.is_context_stage()) for r in requests]), which decide every
+    row. Without them, rows of several tokens are prefill rows and a
+    one-token row at first index 0 is the chunk of a one-token prompt; a
+    one-token row at first index f > 0 is a decode row only if its page
+    list (pages_per_row, of page_size tokens) is too short to hold position
+    f, which the table of a prefill chunk, cut to ceil((f + 1) / page_size)
+    pages (kunserve/block_manager.py:786-795), always holds. Any other such
+    row could be either (the last chunk of a prompt one token longer than a
+    chunk multiple, or a decode row), and guessing would write its K/V one
+    position off: ValueError.
     """
     first = np.asarray(first_token_indexes, dtype=np.int64)
     ql = np.asarray(q_lens, dtype=np.int64)
     decode = decode_rows(first_token_indexes, q_lens, is_prefill_requests, use_tensor_cores,
-                         is_context_stage)
+                         is_context_stage, pages_per_row, page_size)
     if np.any(decode & (ql != 1)):
         bad = int(np.argmax(decode & (ql != 1)))
         raise ValueError(f"row {bad}: a decode row takes exactly one input token, got {ql[bad]}")
@@ -198,9 +202,11 @@ def kv_lens_for_step(first_token_indexes: Sequence[int], q_lens: Sequence[int],
 
 def decode_rows(first_token_indexes: Sequence[int], q_lens: Sequence[int],
                 is_prefill_requests: Sequence[int], use_tensor_cores: bool = False,
-                is_context_stage: Optional[Sequence[int]] = None) -> np.ndarray:
+                is_context_stage: Optional[Sequence[int]] = None,
+                pages_per_row: Optional[Sequence[int]] = None,
+                page_size: int = 0) -> np.ndarray:
     """Boolean mask of the decode rows of a step, by the rule of
-    kv_lens_for_step."""
+    kv_lens_for_step (which raises where this does)."""
     first = np.asarray(first_token_indexes, dtype=np.int64)
     ql = np.asarray(q_lens, dtype=np.int64)
     flag = np.asarray(is_prefill_requests, dtype=np.int64)
@@ -211,9 +217,24 @@ def decode_rows(first_token_indexes: Sequence[int], q_lens: Sequence[int],
         if stage.shape != first.shape:
             raise ValueError("is_context_stage differs in length from the other row arguments")
         return stage == 0
-    if use_tensor_cores:
-        return (flag == 0) | ((ql == 1) & (first > 0))
-    return flag == 0
+    if not use_tensor_cores:
+        return flag == 0
+    open_rows = (flag != 0) & (ql == 1) & (first > 0)
+    settled = np.zeros_like(open_rows)
+    if pages_per_row is not None:
+        pages = np.asarray(pages_per_row, dtype=np.int64)
+        if pages.shape != first.shape:
+            raise ValueError("pages_per_row differs in length from the other row arguments")
+        if page_size <= 0:
+            raise ValueError("pages_per_row needs the page_size")
+        settled = open_rows & (pages * page_size <= first)
+    if np.any(open_rows & ~settled):
+        bad = int(np.argmax(open_rows & ~settled))
+        raise ValueError(
+            f"row {bad}: with use_tensor_cores every row is flagged as prefill, and a one-token "
+            f"row at first index {int(first[bad])} may be a decode row or the last chunk of a "
+            f"prompt; pass is_context_stage (each row's request.is_context_stage())")
+    return (flag == 0) | settled
 
 
 def csr_from_lists(pages_of_reqs: Sequence[Sequence[int]], kv_len: np.ndarray,
@@ -509,24 +530,39 @@ def rope_append_kv(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.T
     return q
 
 
+def _check_row_map(m: Optional[torch.Tensor], n: int, device: torch.device, what: str) -> None:
+    if m is not None and (m.dtype != torch.int32 or m.shape != (n,) or m.device != device
+                          or not m.is_contiguous()):
+        raise ValueError(f"{what} must be a contiguous int32 tensor of {n} entries on {device}")
+
+
 def paged_decode(pool: KVPool, layer: int, table: PageTable, q: torch.Tensor, plan: DecodePlan,
                  sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Decode attention of q [num_seqs, Hq, D] over each row's pages."""
+                 workspace: Optional[torch.Tensor] = None,
+                 q_token: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode attention of q [num_seqs, Hq, D] over each row's pages.
+
+    With q_token (device int32 [num_seqs], each entry < q.shape[0]), row b's
+    query and output are token q_token[b] of q and out ([num_tokens, Hq, D]):
+    the decode rows of a mixed step, read and written in place."""
     hq = q.shape[1]
-    if q.shape[0] != table.num_seqs or q.shape[2] != pool.head_dim:
-        raise ValueError(f"q shape {tuple(q.shape)} does not match {table.num_seqs} rows, "
-                         f"head_dim {pool.head_dim}")
+    if q_token is None and q.shape[0] != table.num_seqs:
+        raise ValueError(f"q has {q.shape[0]} tokens for {table.num_seqs} rows")
+    if q.shape[2] != pool.head_dim:
+        raise ValueError(f"q shape {tuple(q.shape)} does not match head_dim {pool.head_dim}")
+    _check_row_map(q_token, table.num_seqs, q.device, "q_token")
     if out is None:
         out = torch.empty_like(q)
+    if out.shape != q.shape:
+        raise ValueError(f"out shape {tuple(out.shape)} differs from q's {tuple(q.shape)}")
     pool.check_dtype(q, out)
     scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(pool.head_dim)
     need = plan.workspace_bytes(pool.head_dim)
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=pool.device)
     qd, od = _tensor3(q), _tensor3(out)
-    _lib.call("kunserve_paged_decode", pool.desc(), layer, table.desc(), ctypes.byref(qd),
-              ctypes.byref(od), hq, ctypes.c_float(scale),
+    _lib.call("kunserve_paged_decode", pool.desc(), layer, table.desc(), _ptr(q_token),
+              ctypes.byref(qd), ctypes.byref(od), hq, ctypes.c_float(scale),
               _ptr(plan.plan), ctypes.byref(plan.info), _ptr(workspace),
               0 if workspace is None else workspace.numel() * workspace.element_size(),
               _stream_ptr(pool.device))
@@ -536,10 +572,18 @@ def paged_decode(pool: KVPool, layer: int, table: PageTable, q: torch.Tensor, pl
 def paged_prefill(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Tensor,
                   q: torch.Tensor, plan: PrefillPlan, sm_scale: Optional[float] = None,
                   out: Optional[torch.Tensor] = None,
-                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Causal chunked-prefill attention of ragged q [num_tokens, Hq, D]."""
+                  workspace: Optional[torch.Tensor] = None,
+                  q_start: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal chunked-prefill attention of ragged q [num_tokens, Hq, D].
+
+    Row b has q_indptr[b+1] - q_indptr[b] tokens, at q_indptr[b] onwards, or
+    with q_start (device int32 [num_seqs]) at q_start[b] onwards: the
+    prefill rows of a mixed step, read and written in place."""
+    _check_row_map(q_start, table.num_seqs, q.device, "q_start")
     if out is None:
         out = torch.empty_like(q)
+    if out.shape != q.shape:
+        raise ValueError(f"out shape {tuple(out.shape)} differs from q's {tuple(q.shape)}")
     pool.check_dtype(q, out)
     scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(pool.head_dim)
     need = plan.workspace_bytes()
@@ -547,7 +591,7 @@ def paged_prefill(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Te
         workspace = torch.empty(need, dtype=torch.uint8, device=pool.device)
     qd, od = _tensor3(q), _tensor3(out)
     _lib.call("kunserve_paged_prefill", pool.desc(), layer, table.desc(), q_indptr.data_ptr(),
-              ctypes.byref(qd), ctypes.byref(od), q.shape[1], ctypes.c_float(scale),
+              _ptr(q_start), ctypes.byref(qd), ctypes.byref(od), q.shape[1], ctypes.c_float(scale),
               _ptr(plan.plan), ctypes.byref(plan.info), _ptr(workspace),
               0 if workspace is None else workspace.numel() * workspace.element_size(),
               _stream_ptr(pool.device))
@@ -557,7 +601,9 @@ def paged_prefill(pool: KVPool, layer: int, table: PageTable, q_indptr: torch.Te
 @dataclass
 class _Subset:
     rows: np.ndarray            # row indices into the batch
-    tokens: Optional[torch.Tensor]  # int32 token indices into q (None: all tokens, in order)
+    # int32 per subset row: its (first) token in q and out; None when the
+    # subset is the whole step, whose rows' tokens are in order
+    tokens: Optional[torch.Tensor]
     table: PageTable
     q_indptr: Optional[torch.Tensor]
     plan: object
@@ -570,8 +616,9 @@ class AttentionStep:
     Per layer: append the new K/V of every row, then decode attention for
     decode rows and causal chunked-prefill attention for the others. Which
     rows decode follows kv_lens_for_step (flag 0; with use_tensor_cores,
-    where every row is flagged, kunserve/request.py:667-670, one-token rows
-    past position 0).
+    where every row is flagged, kunserve/request.py:667-670, the rows' real
+    stages, is_context_stage, and a step whose one-token rows they do not
+    settle raises ValueError).
 
     pool may be a fused view (KVPool.fused_view); id_map then turns the
     page lists' fused ids into its pages, and num_ids bounds those ids.
@@ -598,10 +645,13 @@ class AttentionStep:
             raise ValueError(f"{len(q_lens)} rows but {len(pages_of_reqs)} page lists")
         if np.any(q_lens < 1):
             raise ValueError("every row needs at least one input token")
+        pages_per_row = [len(p) for p in pages_of_reqs]
         self.kv_len = kv_lens_for_step(first_token_indexes, q_lens, is_prefill_requests,
-                                       use_tensor_cores, is_context_stage)
+                                       use_tensor_cores, is_context_stage, pages_per_row,
+                                       pool.page_size)
         is_decode = decode_rows(first_token_indexes, q_lens, is_prefill_requests,
-                                use_tensor_cores, is_context_stage)
+                                use_tensor_cores, is_context_stage, pages_per_row,
+                                pool.page_size)
         self.q_indptr_host = np.zeros(len(q_lens) + 1, dtype=np.int32)
         np.cumsum(q_lens, out=self.q_indptr_host[1:])
         self.num_tokens = int(self.q_indptr_host[-1])
@@ -640,9 +690,7 @@ class AttentionStep:
                 table, tokens, qi = self.table, None, self.q_indptr_host
             else:
                 table = sub_table(pre_rows)
-                tokens = np.concatenate([np.arange(self.q_indptr_host[i],
-                                                   self.q_indptr_host[i + 1])
-                                         for i in pre_rows]).astype(np.int32)
+                tokens = self.q_indptr_host[pre_rows].astype(np.int32)
                 qi = np.zeros(pre_rows.size + 1, dtype=np.int32)
                 np.cumsum(q_lens[pre_rows], out=qi[1:])
             plan = PrefillPlan(qi, self.kv_len[pre_rows], num_qo_heads, pool.num_kv_heads, dev,
@@ -703,22 +751,14 @@ class AttentionStep:
             append_kv(self.pool, local, self.table, self.q_indptr, k, v)
         if out is None:
             out = torch.empty_like(q)
+        # Each kernel reads its rows' q and writes their out in place: in a
+        # mixed step through the subset's row -> token map.
         if self.decode is not None:
             d = self.decode
-            if d.tokens is None:
-                paged_decode(self.pool, local, d.table, q, d.plan, self.scale, out=out,
-                             workspace=self.workspace)
-            else:
-                out[d.tokens] = paged_decode(self.pool, local, d.table,
-                                             q.index_select(0, d.tokens), d.plan,
-                                             self.scale, workspace=self.workspace)
+            paged_decode(self.pool, local, d.table, q, d.plan, self.scale, out=out,
+                         workspace=self.workspace, q_token=d.tokens)
         if self.prefill is not None:
             p = self.prefill
-            if p.tokens is None:
-                paged_prefill(self.pool, local, p.table, p.q_indptr, q, p.plan, self.scale,
-                              out=out, workspace=self.workspace)
-            else:
-                out[p.tokens] = paged_prefill(self.pool, local, p.table, p.q_indptr,
-                                              q.index_select(0, p.tokens), p.plan,
-                                              self.scale, workspace=self.workspace)
+            paged_prefill(self.pool, local, p.table, p.q_indptr, q, p.plan, self.scale,
+                          out=out, workspace=self.workspace, q_start=p.tokens)
         return out

@@ -224,20 +224,28 @@ def kv_scatter(k_pool: np.ndarray, v_pool: np.ndarray, layer_begin: int, layer_e
 
 def kv_lens_for_step(first_token_indexes: Sequence[int], q_lens: Sequence[int],
                      is_prefill_requests: Sequence[int], use_tensor_cores: bool = False,
-                     is_context_stage: Sequence[int] | None = None) -> np.ndarray:
+                     is_context_stage: Sequence[int] | None = None,
+                     pages_per_row: Sequence[int] | None = None,
+                     page_size: int = 0) -> np.ndarray:
     """kv_len after append. Prefill rows: first = prefill_begin_index, so
     first + q_len; decode rows: first = prompt_len + output_len, which
     already counts the token being decoded (kunserve/request.py:414-462).
     With use_tensor_cores every row is flagged prefill
-    (kunserve/request.py:667-670); a one-token row past position 0 is then
-    read as a decode row. is_context_stage, when given, is each row's real
-    stage and decides instead."""
+    (kunserve/request.py:667-670). is_context_stage, when given, is each
+    row's real stage and decides. Otherwise a one-token row past position 0
+    is a decode row only when its table cannot hold position `first` (a
+    prefill chunk's table holds ceil((first + 1) / page_size) pages,
+    kunserve/block_manager.py:786-795); when it can, the row is ambiguous
+    and ValueError is raised."""
     out = []
     for b, (f, ql, flag) in enumerate(zip(first_token_indexes, q_lens, is_prefill_requests)):
         if is_context_stage is not None:
             decode = not is_context_stage[b]
-        elif use_tensor_cores:
-            decode = (not flag) or (ql == 1 and f > 0)
+        elif use_tensor_cores and flag and ql == 1 and f > 0:
+            if pages_per_row is None or pages_per_row[b] * page_size > f:
+                raise ValueError(f"row {b}: one-token row at {f} is ambiguous under "
+                                 f"use_tensor_cores")
+            decode = True
         else:
             decode = not flag
         out.append(f if decode else f + ql)

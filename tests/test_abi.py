@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_error_channel():
     lib = _lib.lib()
-    assert lib.kunserve_version() == 100
+    assert lib.kunserve_version() == 300
     assert lib.kunserve_last_error() == b""
 
 

@@ -218,4 +218,16 @@ def test_llama_op_pmm_drop_and_restore(device):
         op.pforward(2, 21, 2 * base + 8, 0, 2, [[0] * n for n in q_lens], first, flags, pages)
     with pytest.raises(IndexError):
         op.pforward(2, 21, 2 * base, 0, 2, [[0] * n for n in q_lens], first, flags, pages)
+    # the restore leaves the group: kv_exchange_scatter takes unfused ids
+    # again, whole pages of all layers (block_manager.py:347-348)
+    assert op.fusion_size == 1
+    before_k, before_v = op.pool.k.clone(), op.pool.v.clone()
+    packed = op.kv_exchange_pack([3, 9], 1, 4)
+    op.kv_exchange_scatter([5, 12], 1, 4, packed)
+    torch.cuda.synchronize()
+    want_k, want_v = before_k.clone(), before_v.clone()
+    want_k[[5, 12], 1:4] = before_k[[3, 9], 1:4]
+    want_v[[5, 12], 1:4] = before_v[[3, 9], 1:4]
+    assert torch.equal(op.pool.k.view(torch.int16), want_k.view(torch.int16))
+    assert torch.equal(op.pool.v.view(torch.int16), want_v.view(torch.int16))
     op.pmm.close()

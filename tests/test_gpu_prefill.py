@@ -51,10 +51,18 @@ def run_prefill(pool, layer, q_lens, kv, indptr, indices, q_indptr, hq, device, 
     return q, out
 
 
-def oracle_prefill(pool, layer, q, q_indptr, indptr, indices, kv):
-    k, v, ip, ix = compact_for_oracle(pool, layer, indptr, indices)
-    return ref.prefill_attention(q.cpu().numpy(), q_indptr, k, v, 0, ip, ix, kv,
-                                 1.0 / math.sqrt(pool.head_dim))
+def oracle_prefill(pool, layer, q, q_indptr, indptr, indices, kv, rows=None):
+    """The numpy oracle's prefill of every row, or of the rows listed (their
+    q rows concatenated, in that order)."""
+    scale = 1.0 / math.sqrt(pool.head_dim)
+    if rows is None:
+        k, v, ip, ix = compact_for_oracle(pool, layer, indptr, indices)
+        return ref.prefill_attention(q.cpu().numpy(), q_indptr, k, v, 0, ip, ix, kv, scale)
+    k, v, ip, ix = compact_for_oracle(pool, layer, indptr, indices, rows)
+    qs = torch.cat([q[int(q_indptr[b]):int(q_indptr[b + 1])] for b in rows])
+    qi = np.concatenate([[0], np.cumsum([int(q_indptr[b + 1] - q_indptr[b]) for b in rows])])
+    return ref.prefill_attention(qs.cpu().numpy(), qi, k, v, 0, ip, ix, np.asarray(kv)[rows],
+                                 scale)
 
 
 @pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (12, 4)])
@@ -215,13 +223,20 @@ def test_prefill_one_token_rows_equal_decode(device):
     assert max_abs(out, dec) <= 1e-3
 
 
-def test_chunked_prefill_workload_sampled(device):
-    """The 16-sequence chunked-prefill workload: every step appends its chunk
-    and attends; two steps are checked against the oracle in full."""
+def test_chunked_prefill_workload_every_step(device):
+    """The 16-sequence chunked-prefill workload (prompts U[512, 4096],
+    prefixes U[0, 2048], chunk 512; kunserve/request.py:368-391): every step
+    appends its chunk and attends, and every row of every step is checked
+    against the fp32 PyTorch restatement run on the device
+    (oracle.torch_cpu.prefill_attention, pinned against the numpy oracle on
+    the CPU); the first and last steps are also checked in full, and one row
+    of every other step, against the numpy oracle."""
+    from oracle import torch_cpu
+
     w = workloads.chunked_prefill()
     pool = random_pool(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device, 10)
     steps = w.steps()
-    checked = {0, len(steps) - 1}
+    assert len(steps) == 8
     for i, (rows, ql, kv) in enumerate(steps):
         pages = [w.pages[r] for r in rows]
         q_indptr = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
@@ -236,9 +251,21 @@ def test_chunked_prefill_workload_sampled(device):
         append_kv(pool, 0, table, qi, k_new, v_new)
         q = random_tensor((T, w.num_qo_heads, w.head_dim), device, 300 + i)
         out = paged_prefill(pool, 0, table, qi, q, PrefillPlan(q_indptr, kv, w.num_qo_heads, w.num_kv_heads, device))
-        if i in checked:
-            want = oracle_prefill(pool, 0, q, q_indptr, indptr, indices, kv)
-            assert max_abs(out, want) <= ATOL
+        want = torch_cpu.prefill_attention(q, q_indptr, pool.k, pool.v, 0, indptr, indices, kv,
+                                           1 / math.sqrt(w.head_dim))
+        err = float((out.float() - want).abs().max())
+        assert err <= ATOL, (i, err)
+        if i in (0, len(steps) - 1):
+            sample = None                              # the whole step
+        else:
+            sample = [int(np.argmax(kv))]              # the row deepest into its prompt
+        want_np = oracle_prefill(pool, 0, q, q_indptr, indptr, indices, kv, rows=sample)
+        if sample is None:
+            assert max_abs(out, want_np) <= ATOL, i
+        else:
+            b = sample[0]
+            lo, hi = int(q_indptr[b]), int(q_indptr[b + 1])
+            assert max_abs(out[lo:hi], want_np) <= ATOL, i
 
 
 @pytest.mark.parametrize("head_size", [64, 128, 256])

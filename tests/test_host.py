@@ -21,24 +21,57 @@ def test_kv_lens_rule_matches_oracle():
 
 def test_kv_lens_with_tensor_cores():
     """use_tensor_cores flags every row as prefill (kunserve/request.py:667-670).
-    A decode row (first = prompt_len + output_len) keeps kv_len = first, so
-    its token lands at first - 1 and stays inside ceil(first / bs) blocks
-    (kunserve/block_manager.py:493-500); chunks of several tokens and a
-    one-token prompt are prefill. The positions every row writes over whole
-    request lifecycles are checked in test_oracle.py."""
+    Given the rows' real stages, a decode row (first = prompt_len +
+    output_len) keeps kv_len = first, so its token lands at first - 1
+    inside ceil(first / bs) blocks (kunserve/block_manager.py:493-500), and
+    a chunk row takes first + q_len. Without them, chunks of several tokens
+    and a one-token prompt are still prefill; a one-token row past position
+    0 is decode only when its page list cannot hold position `first`, else
+    it raises. Whole request lifecycles are checked in test_oracle.py."""
     rng = np.random.default_rng(1)
     first = rng.integers(0, 5000, 200)
     ql = np.where(rng.random(200) < 0.5, 1, rng.integers(2, 600, 200))
+    stage = np.where(ql == 1, rng.integers(0, 2, 200), 1)
     flag = np.ones(200, dtype=np.int64)
-    got = kv_lens_for_step(first, ql, flag, use_tensor_cores=True)
-    assert np.array_equal(got, ref.kv_lens_for_step(first, ql, flag, use_tensor_cores=True))
-    assert kv_lens_for_step([64], [1], [1], use_tensor_cores=True).tolist() == [64]
-    assert kv_lens_for_step([0], [1], [1], use_tensor_cores=True).tolist() == [1]
-    assert kv_lens_for_step([64], [7], [1], use_tensor_cores=True).tolist() == [71]
+    got = kv_lens_for_step(first, ql, flag, True, stage)
+    assert np.array_equal(got, ref.kv_lens_for_step(first, ql, flag, True, stage))
+    assert np.array_equal(got, np.where(stage == 1, first + ql, first))
     # the rows' real stages decide when given
     assert kv_lens_for_step([64], [1], [1], True, is_context_stage=[1]).tolist() == [65]
+    assert kv_lens_for_step([64], [1], [1], True, is_context_stage=[0]).tolist() == [64]
     with pytest.raises(ValueError, match="exactly one"):
         kv_lens_for_step([64], [5], [1], True, is_context_stage=[0])
+    # without them
+    assert kv_lens_for_step([0], [1], [1], use_tensor_cores=True).tolist() == [1]
+    assert kv_lens_for_step([64], [7], [1], use_tensor_cores=True).tolist() == [71]
+    assert kv_lens_for_step([64], [1], [1], True, None, [4], 16).tolist() == [64]
+    for pages in (None, [5]):
+        with pytest.raises(ValueError, match="is_context_stage"):
+            kv_lens_for_step([64], [1], [1], True, None, pages, 16)
+
+
+def test_llama_op_reference_call_raises_under_tensor_cores():
+    """The reference's 13-argument pforward call (kunserve/flash_backend.py:
+    2448-2469) with --use-tensor-cores: every row flagged as prefill and no
+    is_context_stage. A step with a one-token row the page counts cannot
+    settle raises ValueError before any device work; with the rows' real
+    stages the same step is prepared (the kv_len rule is checked here, the
+    device step in tests/test_gpu_boundary.py)."""
+    import torch
+    from kunserve_amd import LlamaOp
+    from kunserve_amd.paged_kv import decode_rows
+
+    op = LlamaOp(64, 2, 8, 4, 16, 128, 1, 1, 8, 4096, 4096, 1, torch.device("cpu"),
+                 use_tensor_cores=True)
+    # rows: the one-token tail chunk of a 513-token prompt (first 512, 33
+    # pages) and a decode row (first 40, 3 pages)
+    first, flags = [512, 40], [1, 1]
+    pages = [list(range(33)), [40, 41, 42]]
+    with pytest.raises(ValueError, match="is_context_stage"):
+        op.pforward(2, 2, 64, 0, 2, [[7], [9]], first, flags, pages, 0, [], [], 0)
+    kv = kv_lens_for_step(first, [1, 1], flags, True, [1, 0], [33, 3], 16)
+    assert kv.tolist() == [513, 40]
+    assert decode_rows(first, [1, 1], flags, True, [1, 0]).tolist() == [False, True]
 
 
 def test_csr_truncates_and_validates():
@@ -139,3 +172,16 @@ def test_reference_class_names_resolve_to_this_package():
     assert hasattr(torch.ops.swapping_ops, "swap")
     with pytest.raises(RuntimeError):   # other gpt_ops names stay native lookups
         torch.classes.gpt_ops.NotAClassOfThisPackage
+
+
+def test_llama_op_restore_leaves_the_fusion_group():
+    """pmm_drop joins a balloon group (fused page ids); pmm_restore leaves it,
+    as restore_from_fusion resets the fusion size
+    (kunserve/block_manager.py:347-348), also for an op without extend
+    memory, whose drop and restore move no pages."""
+    import torch
+    from kunserve_amd import LlamaOp
+
+    op = LlamaOp(16, 4, 8, 2, 16, 128, 1, 1, 8, 4096, 4096, 1, torch.device("cpu"))
+    assert op.pmm_drop(1, 2) == 0 and op.fusion_size == 2
+    assert op.pmm_restore() == [] and op.fusion_size == 1

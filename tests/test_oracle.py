@@ -211,53 +211,90 @@ def _run_lifecycle(kv_rule, prompt_len, chunk, steps, use_tc, page_size=16, real
     positions = []
     for _ in range(steps):
         first, ql, flag, ctx, pages = req.step_args(use_tc, page_size)
-        kv = int(kv_rule([first], [ql], [flag], use_tc, [ctx] if real_stage else None)[0])
+        kv = int(kv_rule([first], [ql], [flag], use_tc, [ctx] if real_stage else None,
+                         [pages], page_size)[0])
         assert kv <= pages * page_size, (first, ql, kv, pages)
         positions.extend(range(kv - ql, kv))
         req.finish_step()
     return positions
 
 
+def _lifecycle_without_stages(kv_rule, prompt_len, chunk, steps, page_size):
+    """--use-tensor-cores without the rows' real stages: at every step the
+    rule either raises ValueError or gives the kv_len the real stage gives.
+    Returns the number of steps that raised."""
+    req = Request(prompt_len, chunk)
+    raised = 0
+    for _ in range(steps):
+        first, ql, flag, ctx, pages = req.step_args(True, page_size)
+        want = int(ref.kv_lens_for_step([first], [ql], [flag], True, [ctx])[0])
+        try:
+            got = int(kv_rule([first], [ql], [flag], True, None, [pages], page_size)[0])
+        except ValueError:
+            raised += 1
+        else:
+            assert got == want, (prompt_len, chunk, first, ql, pages)
+        req.finish_step()
+    return raised
+
+
 def test_kv_len_rule_against_request_lifecycle():
-    for use_tc in (False, True):
-        pos = _run_lifecycle(ref.kv_lens_for_step, 37, 16, 8, use_tc)
-        # Every token position is appended exactly once, in order.
-        assert pos == list(range(len(pos)))
+    pos = _run_lifecycle(ref.kv_lens_for_step, 37, 16, 8, False)
+    # Every token position is appended exactly once, in order.
+    assert pos == list(range(len(pos)))
+    pos = _run_lifecycle(ref.kv_lens_for_step, 37, 16, 8, True, real_stage=True)
+    assert pos == list(range(len(pos)))
 
 
 def test_kv_len_rule_with_tensor_cores_over_random_lifecycles():
     """--use-tensor-cores flags every row as prefill (request.py:667-670):
-    over random prompts and chunk sizes, every position is still appended
-    exactly once and inside the blocks the table holds, for the oracle and
-    for the library's rule alike."""
+    given the rows' real stages, every position is appended exactly once and
+    inside the blocks the table holds over random prompts and chunk sizes,
+    one-token tail chunks included; without them the rule never returns a
+    wrong kv_len, it raises. Oracle and library alike."""
     from kunserve_amd import kv_lens_for_step as lib_rule
 
     rng = np.random.default_rng(11)
+    tails = 0
     for _ in range(300):
         chunk = int(rng.integers(2, 80))
         prompt = int(rng.integers(1, 400))
-        if prompt > 1 and prompt % chunk == 1:
-            prompt += 1          # a one-token tail chunk: see the next test
+        tails += prompt > 1 and prompt % chunk == 1
         for rule in (ref.kv_lens_for_step, lib_rule):
             for ps in (4, 16):
-                pos = _run_lifecycle(rule, prompt, chunk, 12, True, ps)
+                pos = _run_lifecycle(rule, prompt, chunk, 12, True, ps, real_stage=True)
                 assert pos == list(range(len(pos)))
+                _lifecycle_without_stages(rule, prompt, chunk, 12, ps)
+    assert tails > 0
 
 
-def test_one_token_tail_chunk_needs_the_real_stage():
+def test_tensor_cores_without_stages_raises_on_ambiguous_rows():
     """A prompt one token longer than a chunk multiple ends in a one-token
     chunk at first index > 0, which the all-prefill flags cannot tell from a
     decode row; given the rows' real stages the rule appends every position
-    once. A one-token prompt (first index 0) needs no help."""
+    once; without them it raises at that chunk (and at decode rows whose
+    table could hold their position), rather than writing K/V one position
+    off. A decode row whose table is too short for position `first` is
+    settled by its page count, and a one-token prompt (first index 0) needs
+    no help."""
     from kunserve_amd import kv_lens_for_step as lib_rule
 
     for rule in (ref.kv_lens_for_step, lib_rule):
         pos = _run_lifecycle(rule, 33, 16, 6, True, real_stage=True)
-        assert pos == list(range(len(pos)))
-        pos = _run_lifecycle(rule, 1, 16, 5, True)
-        assert pos == list(range(len(pos)))
-        with pytest.raises(AssertionError):
-            assert _run_lifecycle(rule, 33, 16, 6, True) == list(range(37))
+        assert pos == list(range(36))
+        assert _run_lifecycle(rule, 1, 16, 1, True) == [0]
+        with pytest.raises(ValueError, match="is_context_stage|ambiguous"):
+            _run_lifecycle(rule, 33, 16, 6, True)
+        # the tail chunk (first 32, 3 pages of 16) and the decode row at
+        # first 33 (3 pages) raise; the decode row at 48 (3 pages) does not
+        assert rule([48], [1], [1], True, None, [3], 16).tolist() == [48]
+        for first, pages in ((32, 3), (33, 3), (47, 3), (48, 4)):
+            with pytest.raises(ValueError):
+                rule([first], [1], [1], True, None, [pages], 16)
+        # the tail row itself, without page counts
+        with pytest.raises(ValueError):
+            rule([32], [1], [1], True)
+        assert _lifecycle_without_stages(rule, 513, 512, 4, 16) == 3   # all but the first chunk
 
 
 def test_fused_page_ids():
@@ -423,3 +460,52 @@ def test_torch_cpu_restatement_matches_the_oracle():
         got = torch_cpu.decode_attention(torch.from_numpy(q), torch.from_numpy(k),
                                          torch.from_numpy(v), 1, indptr, indices, kv, 0.125)
         np.testing.assert_allclose(got.numpy(), want, rtol=0, atol=1e-5)
+
+
+def test_torch_prefill_restatement_matches_the_oracle():
+    """The PyTorch prefill that the GPU tests run on the device as the
+    full-size reference of the chunked-prefill workload, and that bench.py
+    times as the prefill CPU baseline, computes the oracle's causal prefill
+    (fp32 vs float64: within 1e-5 on fp16 pages), for MHA and GQA, ragged
+    rows with and without prefixes, and a row subset."""
+    from oracle import torch_cpu
+
+    rng = np.random.default_rng(18)
+    npg, L, hkv, ps, d = 60, 2, 2, 16, 64
+    k = rng.standard_normal((npg, L, hkv, ps, d)).astype(np.float16)
+    v = rng.standard_normal((npg, L, hkv, ps, d)).astype(np.float16)
+    q_lens = np.array([1, 33, 7, 64])
+    prefix = np.array([40, 0, 250, 100])
+    kv = prefix + q_lens
+    need = (kv + ps - 1) // ps
+    indptr = np.concatenate([[0], np.cumsum(need)])
+    indices = rng.permutation(npg)[:indptr[-1]]
+    q_indptr = np.concatenate([[0], np.cumsum(q_lens)])
+    for hq in (2, 6):
+        q = rng.standard_normal((int(q_lens.sum()), hq, d)).astype(np.float16)
+        want = ref.prefill_attention(q, q_indptr, k, v, 1, indptr, indices, kv, 0.125)
+        got = torch_cpu.prefill_attention(torch.from_numpy(q), q_indptr, torch.from_numpy(k),
+                                          torch.from_numpy(v), 1, indptr, indices, kv, 0.125)
+        np.testing.assert_allclose(got.numpy(), want, rtol=0, atol=1e-5)
+        part = torch_cpu.prefill_attention(torch.from_numpy(q), q_indptr, torch.from_numpy(k),
+                                           torch.from_numpy(v), 1, indptr, indices, kv, 0.125,
+                                           rows=[2])
+        np.testing.assert_array_equal(part.numpy()[q_indptr[2]:q_indptr[3]],
+                                      got.numpy()[q_indptr[2]:q_indptr[3]])
+        assert not part.numpy()[:q_indptr[2]].any() and not part.numpy()[q_indptr[3]:].any()
+
+
+def test_torch_copy_restatement_matches_the_oracle():
+    """The PyTorch block copy that bench.py times as the remap copy's CPU
+    baseline moves the oracle's bytes."""
+    from oracle import torch_cpu
+
+    rng = np.random.default_rng(19)
+    kp = rng.integers(-30000, 30000, (24, 3, 2, 4, 8)).astype(np.int16)
+    vp = rng.integers(-30000, 30000, (24, 3, 2, 4, 8)).astype(np.int16)
+    src, dst = rng.permutation(12)[:7], 12 + rng.permutation(12)[:7]
+    kt, vt = torch.from_numpy(kp.copy()), torch.from_numpy(vp.copy())
+    torch_cpu.copy_blocks(kt, vt, src, dst)
+    ref.copy_blocks(kp, src, dst)
+    ref.copy_blocks(vp, src, dst)
+    assert np.array_equal(kt.numpy(), kp) and np.array_equal(vt.numpy(), vp)

@@ -29,10 +29,11 @@ def _decode_both(pool, table, q, plan, device):
     out = torch.full_like(q, float("nan"))
     qd, od, rd = _tensor3(q), _tensor3(out), _tensor3(ref_out)
     scale = ctypes.c_float(1 / 128 ** 0.5)
-    _lib.call("kunserve_paged_decode", pool.desc(), 1, table.desc(), ctypes.byref(qd),
+    _lib.call("kunserve_paged_decode", pool.desc(), 1, table.desc(), None, ctypes.byref(qd),
               ctypes.byref(rd), hq, scale, plan.plan.data_ptr(), ctypes.byref(plan.info),
               ws.data_ptr(), ws.numel(), _stream(device))
-    _lib.call("kunserve_paged_decode_noalloc", pool.desc(), 1, table.desc(), ctypes.byref(qd),
+    _lib.call("kunserve_paged_decode_noalloc", pool.desc(), 1, table.desc(), None,
+              ctypes.byref(qd),
               ctypes.byref(od), hq, scale, plan.plan.data_ptr(), ctypes.byref(plan.info),
               _stream(device))
     torch.cuda.synchronize()
@@ -70,11 +71,15 @@ def test_noalloc_decode_rejects_plans_beyond_its_scratch(device):
     plan = DecodePlan(kv, hq, hkv, device, part_tokens=256)
     assert plan.workspace_bytes(128) > limit
     pool = random_pool(8, 2, hkv, 16, 128, device, 4)
-    table = table_from_csr(np.zeros(97, np.int32), np.zeros(0, np.int32), kv, device)
+    # a real table (every row on page 0 of the pool), so that a call past the
+    # host check would still read only pool memory
+    per_row = (8192 + 15) // 16
+    table = table_from_csr(np.arange(97, dtype=np.int32) * per_row,
+                           np.zeros(96 * per_row, np.int32), kv, device)
     q = random_tensor((96, hq, 128), device, 5)
     qd, od = _tensor3(q), _tensor3(torch.empty_like(q))
     with pytest.raises(_lib.KunserveError) as e:
-        _lib.call("kunserve_paged_decode_noalloc", pool.desc(), 1, table.desc(),
+        _lib.call("kunserve_paged_decode_noalloc", pool.desc(), 1, table.desc(), None,
                   ctypes.byref(qd), ctypes.byref(od), hq, ctypes.c_float(0.088),
                   plan.plan.data_ptr(), ctypes.byref(plan.info), _stream(device))
     assert e.value.code == _lib.ENOSPC
