@@ -522,14 +522,46 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16):
         for table, qi, plan, q, k, v, out in steps:
             ks.rope_append_kv(pool, 0, table, qi, q, k, v, inv_freq)
 
-    rope = None
+    # The append alone over the same steps: k and v read, then written.
+    append_bytes = sum(4 * q.shape[0] * w.num_kv_heads * w.head_dim * 2
+                       for table, qi, plan, q, k, v, out in steps)
+
+    def run_append():
+        for table, qi, plan, q, k, v, out in steps:
+            ks.append_kv(pool, 0, table, qi, k, v)
+
+    rope = append = None
     if page_size == 16 and dtype == torch.float16:
         run_rope()
-        rope_reps = 4
-        rope_ms = region_ms(lambda: [run_rope() for _ in range(rope_reps)], device) / rope_reps
+        run_append()
+        reps_bw = 8
+        rope_ms = region_ms(lambda: [run_rope() for _ in range(reps_bw)], device) / reps_bw
+        append_ms = region_ms(lambda: [run_append() for _ in range(reps_bw)], device) / reps_bw
+        gbs = lambda b, ms: b / (ms * 1e-3) / 1e9
+        # Reference for launches of this size: a plain device copy of each
+        # step's k and v (the same bytes read and written, one launch per
+        # step and tensor, torch's copy kernel).
+        dsts = [(torch.empty_like(k), torch.empty_like(v)) for _, _, _, _, k, v, _ in steps]
+
+        def run_copy():
+            for (table, qi, plan, q, k, v, out), (dk, dv) in zip(steps, dsts):
+                dk.copy_(k)
+                dv.copy_(v)
+        run_copy()
+        copy_ms = region_ms(lambda: [run_copy() for _ in range(reps_bw)], device) / reps_bw
+        del dsts
         log(f"rope + append prologue: {rope_ms:.3f} ms for the 8 steps = "
-            f"{rope_bytes / (rope_ms * 1e-3) / 1e9:.1f} GB/s")
-        rope = {"ms": rope_ms, "bytes": rope_bytes, "gbs": rope_bytes / (rope_ms * 1e-3) / 1e9}
+            f"{gbs(rope_bytes, rope_ms):.1f} GB/s; append alone {append_ms:.3f} ms = "
+            f"{gbs(append_bytes, append_ms):.1f} GB/s; a plain copy of the steps' k and v "
+            f"{copy_ms:.3f} ms = {gbs(append_bytes, copy_ms):.1f} GB/s")
+        rope = {"ms": rope_ms, "bytes": rope_bytes, "gbs": gbs(rope_bytes, rope_ms),
+                "hbm_frac": gbs(rope_bytes, rope_ms) / HBM_PEAK_GBS,
+                "launches": len(steps) * reps_bw}
+        append = {"ms": append_ms, "bytes": append_bytes, "gbs": gbs(append_bytes, append_ms),
+                  "hbm_frac": gbs(append_bytes, append_ms) / HBM_PEAK_GBS,
+                  "launches": len(steps) * reps_bw,
+                  "plain_copy_same_bytes_gbs": gbs(append_bytes, copy_ms),
+                  "frac_of_plain_copy": copy_ms / append_ms}
 
     reps = max(1, args.steps // 4)
     for _ in range(max(1, args.warmup)):
@@ -578,7 +610,8 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16):
             "ms_with_append": elapsed * 1e3, "attention_ms": attn_ms, "tflops": tflops,
             "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS, "page_size": page_size,
             "algorithmic_bytes": nbytes, "flop_per_byte": flops / nbytes,
-            "roofline_ms": roof_ms, "roofline_frac": roof_ms / attn_ms, "rope_append": rope}
+            "roofline_ms": roof_ms, "roofline_frac": roof_ms / attn_ms, "rope_append": rope,
+            "append": append}
 
 
 def mfma_ceiling(device, settle_s=0.5, reps=64):

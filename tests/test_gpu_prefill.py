@@ -41,6 +41,43 @@ def test_append_bit_exact(device):
     assert np.array_equal(pool.v.cpu().numpy().view(np.int16), v0.view(np.int16))
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("num_rows,hkv", [(5, 8), (70, 1), (70, 8)])
+def test_append_tiles_rows_and_skipped_tokens(device, d, num_rows, hkv):
+    """The append kernel's token tiles against the oracle: fewer than 64
+    rows (rows found by a ballot over q_indptr) and 70 rows (binary search),
+    empty rows, tiles that straddle rows and pages, step tokens no row owns
+    (num_tokens > q_indptr[-1]), and page ids outside the pool, whose tokens
+    are dropped (the oracle writes them to a spare page that the check then
+    ignores)."""
+    rng = np.random.default_rng(num_rows * 1000 + d + hkv)
+    ps, layers = 16, 2
+    q_lens = rng.integers(0, 40, num_rows)
+    q_lens[::7] = 0                                    # empty rows
+    prefixes = rng.integers(0, 100, num_rows)
+    kv = (prefixes + q_lens).astype(np.int32)
+    need = (kv + ps - 1) // ps
+    npg = int(need.sum()) + 4
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    bad = rng.choice(indptr[-1], size=3, replace=False)
+    indices[bad[0]], indices[bad[1]], indices[bad[2]] = -1, npg, npg + 1000
+    q_indptr = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    T = int(q_indptr[-1]) + 9                          # 9 trailing tokens no row owns
+    pool = random_pool(npg, layers, hkv, ps, d, device, 1)
+    kn, vn = random_tensor((T, hkv, d), device, 2), random_tensor((T, hkv, d), device, 3)
+    k0, v0 = pool.k.cpu().numpy(), pool.v.cpu().numpy()
+    append_kv(pool, 1, table_from_csr(indptr, indices, kv, device),
+              torch.from_numpy(q_indptr).to(device), kn, vn)
+    torch.cuda.synchronize()
+    spare = np.concatenate([k0, k0[:1]]), np.concatenate([v0, v0[:1]])
+    ids = np.where((indices >= 0) & (indices < npg), indices, npg).astype(np.int32)
+    ref.append_kv(spare[0], spare[1], 1, indptr, ids, kv, q_indptr, kn.cpu().numpy(),
+                  vn.cpu().numpy())
+    assert np.array_equal(pool.k.cpu().numpy().view(np.int16), spare[0][:npg].view(np.int16))
+    assert np.array_equal(pool.v.cpu().numpy().view(np.int16), spare[1][:npg].view(np.int16))
+
+
 def run_prefill(pool, layer, q_lens, kv, indptr, indices, q_indptr, hq, device, seed):
     T = int(q_indptr[-1])
     q = random_tensor((T, hq, pool.head_dim), device, seed)
