@@ -95,7 +95,7 @@ class LaunchTimer:
 # ------------------------------------------------------------------ decode
 
 
-def measure_decode(w, pool, layers, args, device, indices_override=None):
+def measure_decode(w, pool, layers, args, device, indices_override=None, q_scale=1.0):
     """Times paged_decode over `layers` of `pool` for workload `w`: one step
     is one launch per layer. Returns the timing and the objects used."""
     import kunserve_amd as ks
@@ -109,8 +109,8 @@ def measure_decode(w, pool, layers, args, device, indices_override=None):
     plan = ks.DecodePlan(w.kv_len, w.num_qo_heads, w.num_kv_heads, device,
                          part_tokens=args.part_tokens)
     ws = torch.zeros(max(plan.workspace_bytes(w.head_dim), 1), dtype=torch.uint8, device=device)
-    qs = [torch.randn((w.batch, w.num_qo_heads, w.head_dim), generator=gen, device=device
-                      ).to(pool.k.dtype) for _ in layers]
+    qs = [(torch.randn((w.batch, w.num_qo_heads, w.head_dim), generator=gen, device=device
+                       ) * q_scale).to(pool.k.dtype) for _ in layers]
     out = torch.empty_like(qs[0])
 
     def step():
@@ -168,6 +168,163 @@ def bench_decode(args, device):
     return res
 
 
+def bench_single_layer(args, device):
+    """Single-layer decode (batch 8, 32/32 heads, contexts U[128, 512],
+    tables from a permutation of a 512-page pool, Q/K/V ~ N(0,1)/sqrt(128)):
+    the shape the reference's CPU path runs whole. Times many back-to-back
+    launches (one launch moves about 34 MB, so launch overhead is a large
+    share), checks the output against the numpy oracle, and times the
+    PyTorch-CPU restatement of the whole layer and the one-thread numpy
+    oracle beside it."""
+    import copy
+
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+    from oracle import paged_attention_ref as ref
+    from oracle import torch_cpu
+    from threadpoolctl import threadpool_limits
+
+    w = workloads.single_layer_decode()
+    scale = 1 / math.sqrt(w.head_dim)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed)
+    pool = ks.KVPool.allocate(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device)
+    for t in (pool.k, pool.v):
+        t.copy_(torch.randn(t.shape, generator=gen, device=device) * scale)
+    a = copy.copy(args)
+    a.steps = max(args.steps, 200)
+    res = measure_decode(w, pool, [0], a, device, q_scale=scale)
+    indptr, indices = w.csr()
+    q = res["qs"][0]
+    out = ks.paged_decode(pool, 0, res["table"], q, res["plan"])
+    kh, vh, qh = pool.k.cpu(), pool.v.cpu(), q.cpu()
+    want = ref.decode_attention(qh.numpy(), kh.numpy(), vh.numpy(), 0, indptr, indices,
+                                w.kv_len, scale)
+    err = float(np.max(np.abs(out.float().cpu().numpy() - want)))
+    log(f"single-layer decode: {w.name}: per launch {res['launch_ms'] * 1e3:.2f} us = "
+        f"{res['achieved']:.1f} GB/s ({res['achieved'] / HBM_PEAK_GBS * 100:.1f}% of HBM peak); "
+        f"max-abs vs the oracle {err:.2e}")
+    if err > 2e-3:
+        print(f"single-layer decode check failed: max-abs {err}", file=sys.stderr)
+        sys.exit(1)
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = cpu_threads()
+        prev = torch.get_num_threads()
+        torch.set_num_threads(threads)
+        try:
+            med, times = cpu_timed(lambda: torch_cpu.decode_attention(
+                qh, kh, vh, 0, indptr, indices, w.kv_len, scale), args.cpu_budget / 8)
+        finally:
+            torch.set_num_threads(prev)
+        with threadpool_limits(limits=1):
+            np_med, _ = cpu_timed(lambda: ref.decode_attention(
+                qh.numpy(), kh.numpy(), vh.numpy(), 0, indptr, indices, w.kv_len, scale,
+                dtype=np.float32), 0.5)
+        nb = res["bytes_per_layer"]
+        cpu = {"value": nb / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"PyTorch-CPU restatement (oracle/torch_cpu.py), fp32 on fp16 pages, "
+                         f"{threads} threads: the whole workload ({w.batch} rows, one layer, "
+                         f"{nb / 1e6:.1f} MB); median of {len(times)} runs after one warm-up; "
+                         f"{med * 1e3:.2f} ms per run",
+               "runs_s": [round(t, 5) for t in times],
+               "numpy_one_thread_gbs": nb / np_med / 1e9}
+        log(f"single-layer decode cpu baseline: {cpu['value']:.3f} GB/s ({cpu['sample']})")
+    return {"workload": w.name, "launch_us": res["launch_ms"] * 1e3, "gbs": res["achieved"],
+            "hbm_frac": res["achieved"] / HBM_PEAK_GBS, "bytes_per_launch": res["bytes_per_layer"],
+            "launches_timed": a.steps, "max_abs_vs_oracle": err, "cpu_baseline": cpu}
+
+
+def bench_mixed(args, device, layers=4):
+    """One pforward attention step that mixes the chunked-prefill workload's
+    first step (16 chunks of up to 512 tokens on prefixes U[0, 2048]) with
+    the Llama-2-7B decode workload's 64 decode rows, as the reference's
+    scheduler batches running decodes with prefill chunks
+    (kunserve/flash_backend.py:1870-1950; row arguments of
+    kunserve/request.py:654-670). AttentionStep runs it per layer: append,
+    then decode and chunked-prefill attention, each reading q and writing
+    out in place through its row -> token map. Timed per layer against the
+    same two row sets run as steps of their own, with and without the
+    append."""
+    import kunserve_amd as ks
+    from kunserve_amd import workloads
+
+    pw, dw = workloads.chunked_prefill(), workloads.llama2_7b_decode()
+    rows, ql, kv = pw.steps()[0]
+    ps, half = pw.page_size, pw.num_pages
+    rng = np.random.default_rng(1006)
+    # prefill rows keep their pages in [0, 8192); decode rows get disjoint ones above
+    dec_pages = [half + p for p in workloads._tables(rng, dw.kv_len, ps, half)]
+    pool = ks.KVPool.allocate(2 * half, layers, pw.num_kv_heads, ps, pw.head_dim, device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(1006)
+    fill_random_(pool.k, gen)
+    fill_random_(pool.v, gen)
+    need = (kv + ps - 1) // ps
+    pre = dict(q_lens=ql.tolist(), first=(kv - ql).tolist(), flags=[1] * len(rows),
+               pages=[pw.pages[r][:n].tolist() for r, n in zip(rows, need)])
+    dec = dict(q_lens=[1] * dw.batch, first=dw.kv_len.tolist(), flags=[0] * dw.batch,
+               pages=[p.tolist() for p in dec_pages])
+    mixed = {k: dec[k] + pre[k] for k in dec}
+    hq, hkv, d = pw.num_qo_heads, pw.num_kv_heads, pw.head_dim
+
+    def make(spec):
+        step = ks.AttentionStep(pool, hq, spec["q_lens"], spec["first"], spec["flags"],
+                                spec["pages"])
+        T = step.num_tokens
+        t = [torch.randn((T, h, d), generator=gen, device=device).half() for h in (hq, hkv, hkv)]
+        return step, t, torch.empty_like(t[0])
+
+    def attention(step, q, out, layer):
+        # AttentionStep.run without its append
+        if step.decode is not None:
+            sd = step.decode
+            ks.paged_decode(pool, layer, sd.table, q, sd.plan, step.scale, out=out,
+                            workspace=step.workspace, q_token=sd.tokens)
+        if step.prefill is not None:
+            sp = step.prefill
+            ks.paged_prefill(pool, layer, sp.table, sp.q_indptr, q, sp.plan, step.scale,
+                             out=out, workspace=step.workspace, q_start=sp.tokens)
+
+    # The three steps are timed in alternation, one pass over the layers
+    # each, and the medians reported: prefill attention runs at the part's
+    # power limit, and its clock drifts over a run by several percent.
+    built = {name: make(spec) for name, spec in (("mixed", mixed), ("decode", dec),
+                                                   ("prefill", pre))}
+    full = {n: (lambda st=st, t=t, o=o: [st.run(l, *t, out=o) for l in range(layers)])
+            for n, (st, t, o) in built.items()}
+    attn = {n: (lambda st=st, t=t, o=o: [attention(st, t[0], o, l) for l in range(layers)])
+            for n, (st, t, o) in built.items()}
+    for n in built:
+        full[n]()
+    torch.cuda.synchronize()
+    samples = {n: {"full": [], "attn": []} for n in built}
+    for _ in range(max(5, args.steps // 2)):
+        for n in built:
+            samples[n]["full"].append(region_ms(full[n], device) / layers)
+            samples[n]["attn"].append(region_ms(attn[n], device) / layers)
+    res = {n: {"tokens": built[n][0].num_tokens,
+               "ms_per_layer": float(np.median(samples[n]["full"])),
+               "attention_ms_per_layer": float(np.median(samples[n]["attn"])),
+               "passes": len(samples[n]["attn"])} for n in built}
+    del built, full, attn
+    sep = res["decode"]["attention_ms_per_layer"] + res["prefill"]["attention_ms_per_layer"]
+    sep_full = res["decode"]["ms_per_layer"] + res["prefill"]["ms_per_layer"]
+    out = {"workload": f"{pw.name} first step (16 chunks) + {dw.name.split(' x')[0]} "
+                       f"(64 decode rows), one step, {layers} layers",
+           "layers": layers, "steps": res,
+           "attention_ratio_vs_separate": res["mixed"]["attention_ms_per_layer"] / sep,
+           "ratio_vs_separate_with_append": res["mixed"]["ms_per_layer"] / sep_full}
+    log(f"mixed step: attention {res['mixed']['attention_ms_per_layer'] * 1e3:.1f} us/layer "
+        f"against decode {res['decode']['attention_ms_per_layer'] * 1e3:.1f} + prefill "
+        f"{res['prefill']['attention_ms_per_layer'] * 1e3:.1f} us/layer run apart "
+        f"(ratio {out['attention_ratio_vs_separate']:.3f}); with append "
+        f"{res['mixed']['ms_per_layer'] * 1e3:.1f} us/layer (ratio "
+        f"{out['ratio_vs_separate_with_append']:.3f})")
+    del pool
+    return out
+
+
 def bench_gqa(args, device):
     """Llama-3-8B GQA decode (32 Q / 8 KV heads, batch 128, contexts
     U[1024, 8192]), one layer per launch."""
@@ -184,8 +341,14 @@ def bench_gqa(args, device):
     log(f"gqa decode: {w.name}: per launch {res['launch_ms'] * 1e3:.1f} us = "
         f"{res['achieved']:.1f} GB/s ({res['achieved'] / HBM_PEAK_GBS * 100:.1f}% of HBM peak), "
         f"part_tokens {res['plan'].info.part_tokens}, group {res['plan'].info.group_size}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_decode_sample(w, pool, 0, res["qs"][0], np.arange(0, w.batch, 8),
+                                args.cpu_budget / 4)
+        log(f"gqa decode cpu baseline: {cpu['value']:.3f} GB/s ({cpu['sample']})")
     return {"workload": w.name, "launch_us": res["launch_ms"] * 1e3, "gbs": res["achieved"],
-            "hbm_frac": res["achieved"] / HBM_PEAK_GBS, "bytes_per_launch": res["bytes_per_layer"]}
+            "hbm_frac": res["achieved"] / HBM_PEAK_GBS, "bytes_per_launch": res["bytes_per_layer"],
+            "cpu_baseline": cpu}
 
 
 def bench_bf16_decode(args, device, page_size=16):
@@ -255,14 +418,50 @@ def bench_remap(args, device):
     if not same:
         print("remapped decode differs from the original tables", file=sys.stderr)
         sys.exit(1)
+    cpu_copy = cpu_dec = None
+    if not args.no_cpu_baseline:
+        cpu_dec = cpu_decode_sample(w2, pool, 0, dec["qs"][0], np.arange(0, w2.batch, 16),
+                                    args.cpu_budget / 4)
+        log(f"70b decode cpu baseline: {cpu_dec['value']:.3f} GB/s ({cpu_dec['sample']})")
+        cpu_copy = cpu_copy_sample(r, args.cpu_budget / 4)
+        log(f"block copy cpu baseline: {cpu_copy['value']:.3f} GB/s ({cpu_copy['sample']})")
     return {"copy": {"workload": f"remap copy {len(r.src)} blocks x 2 MiB (K+V)",
                      "ms": copy_ms, "gbs": copy_gbs, "hbm_frac": copy_gbs / HBM_PEAK_GBS,
                      "frac_of_best_ceiling_copy": copy_gbs / max(
-                         ceiling["copy_gbs"], ceiling["memcpy_d2d_gbs"])},
+                         ceiling["copy_gbs"], ceiling["memcpy_d2d_gbs"]),
+                     "cpu_baseline": cpu_copy},
             "copy_ceiling": ceiling,
             "decode": {"workload": w.name, "launch_us": dec["launch_ms"] * 1e3,
                        "gbs": dec["achieved"], "hbm_frac": dec["achieved"] / HBM_PEAK_GBS,
-                       "bit_exact_vs_original_tables": same}}
+                       "bit_exact_vs_original_tables": same, "cpu_baseline": cpu_dec}}
+
+
+def cpu_copy_sample(r, budget_s: float, n: int = 256) -> dict:
+    """The PyTorch-CPU restatement of the remap copy (oracle/torch_cpu.py
+    copy_blocks: index_select then index_copy_ of whole blocks) on host
+    pools of 2n blocks of the remap shape: n random blocks of the first half
+    copied into a random permutation of the second half."""
+    from oracle import torch_cpu
+
+    shape = (2 * n, r.num_layers, r.num_kv_heads, r.page_size, r.head_dim)
+    k = torch.randn(shape, dtype=torch.float32).half()
+    v = torch.randn(shape, dtype=torch.float32).half()
+    rng = np.random.default_rng(r.seed)
+    src, dst = rng.permutation(n), n + rng.permutation(n)
+    nbytes = 2 * 2 * n * k[0].numel() * 2
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        med, times = cpu_timed(lambda: torch_cpu.copy_blocks(k, v, src, dst), budget_s)
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"PyTorch-CPU restatement (oracle/torch_cpu.py copy_blocks), {threads} "
+                      f"threads: {n} random blocks of 2 MiB (K+V) between the halves of a "
+                      f"{2 * n}-block host pool, {nbytes / 2**30:.1f} GiB read + written; median "
+                      f"of {len(times)} runs after one warm-up; {med * 1e3:.1f} ms per run",
+            "runs_s": [round(t, 4) for t in times]}
 
 
 def copy_ceiling(pool, r, reps, device):
@@ -473,6 +672,55 @@ def cpu_baseline(res, budget_s: float) -> dict:
             "numpy_one_thread_gbs": res["bytes_per_layer"] / np_s / 1e9}
 
 
+def cpu_timed(fn, budget_s: float, min_runs: int = 3, max_runs: int = 50):
+    """One warm-up call of fn, then timed calls until at least min_runs ran
+    and budget_s passed (at most max_runs). Returns (median s, runs)."""
+    fn()
+    times = []
+    while len(times) < min_runs or (sum(times) < budget_s and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), times
+
+
+def cpu_decode_sample(w, pool, layer, q, rows, budget_s: float) -> dict:
+    """The PyTorch-CPU restatement (oracle/torch_cpu.py) of decode workload
+    w on the given rows of one layer: their pages are copied to the host,
+    then the restatement runs on all host threads. The rate is the sampled
+    rows' algorithmic bytes (K and V of their tokens once per KV head, q,
+    out and page ids) over the median run."""
+    from oracle import torch_cpu
+
+    rows = np.asarray(rows)
+    indptr, indices = w.csr()
+    lo, hi = indptr[rows], indptr[rows + 1]
+    sub_indptr = np.concatenate([[0], np.cumsum(hi - lo)]).astype(np.int32)
+    ids = np.concatenate([indices[a:b] for a, b in zip(lo, hi)]).astype(np.int64)
+    sel = torch.from_numpy(ids).to(pool.device)
+    k = pool.k[:, layer].index_select(0, sel)[:, None].cpu()
+    v = pool.v[:, layer].index_select(0, sel)[:, None].cpu()
+    qh = q[torch.from_numpy(rows.astype(np.int64)).to(q.device)].cpu()
+    kv = w.kv_len[rows]
+    local = np.arange(ids.size, dtype=np.int32)
+    nbytes = (int(kv.astype(np.int64).sum()) * w.num_kv_heads * w.head_dim * 4
+              + 2 * rows.size * w.num_qo_heads * w.head_dim * 2 + ids.size * 4)
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        med, times = cpu_timed(lambda: torch_cpu.decode_attention(
+            qh, k, v, 0, sub_indptr, local, kv, 1 / math.sqrt(w.head_dim)), budget_s)
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"PyTorch-CPU restatement (oracle/torch_cpu.py), fp32 on fp16 pages, "
+                      f"{threads} threads: {rows.size} of the workload's {w.batch} rows (every "
+                      f"{max(1, w.batch // rows.size)}th), one layer, {nbytes / 1e9:.3f} GB; median "
+                      f"of {len(times)} runs after one warm-up; {med * 1e3:.1f} ms per run",
+            "runs_s": [round(t, 4) for t in times]}
+
+
 # ----------------------------------------------------------------- prefill
 
 
@@ -602,6 +850,10 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16):
     log(f"prefill ({name}, page {page_size}): {len(steps)} chunk steps, {elapsed * 1e3:.3f} ms with "
         f"append; attention {attn_ms:.3f} ms = {tflops:.1f} TFLOP/s "
         f"({tflops / FP16_MFMA_PEAK_TFLOPS * 100:.1f}% of the {name} MFMA peak)")
+    cpu = None
+    if page_size == 16 and dtype == torch.float16 and not args.no_cpu_baseline:
+        cpu = cpu_prefill_sample(w, pool, steps[0], args.cpu_budget / 4)
+        log(f"prefill cpu baseline: {cpu['value']:.4f} TFLOP/s ({cpu['sample']})")
     log(f"prefill ({name}, page {page_size}): {nbytes / 1e9:.2f} GB algorithmic, "
         f"{flops / nbytes:.0f} flop/B against a ridge of "
         f"{FP16_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):.0f}; roofline time "
@@ -611,7 +863,51 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16):
             "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS, "page_size": page_size,
             "algorithmic_bytes": nbytes, "flop_per_byte": flops / nbytes,
             "roofline_ms": roof_ms, "roofline_frac": roof_ms / attn_ms, "rope_append": rope,
-            "append": append}
+            "append": append, "cpu_baseline": cpu}
+
+
+def cpu_prefill_sample(w, pool, step, budget_s: float, every: int = 4) -> dict:
+    """The PyTorch-CPU restatement (oracle/torch_cpu.py prefill_attention) of
+    the chunked-prefill workload's first step on every `every`-th row: the
+    rows' pages and q are copied to the host and the restatement runs on all
+    host threads. The rate is the sampled rows' exact causal flops over the
+    median run."""
+    from oracle import torch_cpu
+
+    rows0, ql0, kv0 = w.steps()[0]
+    table, qi, plan, q, k, v, out = step
+    sel_rows = np.arange(0, len(rows0), every)
+    need = (kv0 + w.page_size - 1) // w.page_size
+    ids = np.concatenate([w.pages[rows0[i]][:need[i]] for i in sel_rows]).astype(np.int64)
+    sub_indptr = np.concatenate([[0], np.cumsum(need[sel_rows])]).astype(np.int32)
+    q_indptr = np.concatenate([[0], np.cumsum(ql0)]).astype(np.int64)
+    q_rows = np.concatenate([np.arange(q_indptr[i], q_indptr[i + 1]) for i in sel_rows])
+    sub_qi = np.concatenate([[0], np.cumsum(ql0[sel_rows])]).astype(np.int32)
+    sel = torch.from_numpy(ids).to(pool.device)
+    kh = pool.k.index_select(0, sel).cpu()
+    vh = pool.v.index_select(0, sel).cpu()
+    qh = q[torch.from_numpy(q_rows).to(q.device)].cpu()
+    kv = kv0[sel_rows]
+    flops = 0
+    for n_q, n_kv in zip(ql0[sel_rows].tolist(), kv.tolist()):
+        flops += n_q * (n_kv - n_q) + n_q * (n_q + 1) // 2
+    flops *= 4 * w.num_qo_heads * w.head_dim
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        med, times = cpu_timed(lambda: torch_cpu.prefill_attention(
+            qh, sub_qi, kh, vh, 0, sub_indptr, np.arange(ids.size, dtype=np.int32), kv,
+            1 / math.sqrt(w.head_dim)), budget_s)
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"PyTorch-CPU restatement (oracle/torch_cpu.py), fp32 on fp16 pages, "
+                      f"{threads} threads: {sel_rows.size} of the first step's {len(rows0)} rows "
+                      f"(every {every}th; {int(ql0[sel_rows].sum())} q rows, "
+                      f"{flops / 1e12:.4f} TFLOP exact causal); median of {len(times)} runs after "
+                      f"one warm-up; {med * 1e3:.1f} ms per run",
+            "runs_s": [round(t, 4) for t in times]}
 
 
 def mfma_ceiling(device, settle_s=0.5, reps=64):
@@ -734,7 +1030,7 @@ def main():
     ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
     ap.add_argument("--only", choices=["decode", "prefill", "prefill256", "gqa", "bf16",
                                        "bf16p256", "bf16prefill", "remap", "pmm", "swap",
-                                       "mfma"],
+                                       "mfma", "single", "mixed"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
@@ -761,6 +1057,12 @@ def main():
     if args.only == "bf16prefill":
         print(json.dumps({"bf16_prefill_page256": bench_prefill(args, device, page_size=256,
                                                                 dtype=torch.bfloat16)}))
+        return
+    if args.only == "single":
+        print(json.dumps({"single_layer_decode": bench_single_layer(args, device)}))
+        return
+    if args.only == "mixed":
+        print(json.dumps({"mixed_step": bench_mixed(args, device)}))
         return
     if args.only == "mfma":
         print(json.dumps({"mfma_ceiling": mfma_ceiling(device)}))
@@ -802,8 +1104,12 @@ def main():
     del dec["pool"], dec["qs"]
     torch.cuda.empty_cache()
     prefill = prefill256 = prefill_bf16 = gqa = bf16 = bf16_256 = remap = pmm = swp = None
-    ceiling = None
+    ceiling = single = mixed = None
     if args.only is None:
+        single = bench_single_layer(args, device)
+        torch.cuda.empty_cache()
+        mixed = bench_mixed(args, device)
+        torch.cuda.empty_cache()
         ceiling = mfma_ceiling(device)
         prefill = bench_prefill(args, device)
         prefill["frac_of_random_operand_ceiling"] = prefill["tflops"] / ceiling["random_tflops"]
@@ -859,6 +1165,8 @@ def main():
             "launch_us": round(dec["launch_ms"] * 1e3, 2),
         },
         "cpu_baseline": cpu,
+        "single_layer_decode": single,
+        "mixed_step": mixed,
         "prefill": prefill,
         "mfma_ceiling": ceiling,
         "prefill_page256": prefill256,
