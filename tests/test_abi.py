@@ -61,6 +61,38 @@ def test_decode_plan_covers_every_token_once():
         assert all((work[work[:, 0] == s, 3] == -1).all() for s in single)
 
 
+def _auto_decode_plan(kv, hq, hkv, num_cus=256):
+    kv = np.asarray(kv, dtype=np.int32)
+    cap = _lib.lib().kunserve_decode_plan_bound(kv.ctypes.data, kv.size)
+    buf = np.zeros(cap, dtype=np.int32)
+    info = _lib.DecodePlanInfo()
+    _lib.call("kunserve_decode_plan", kv.ctypes.data, kv.size, hq, hkv, num_cus, 0,
+              buf.ctypes.data, cap, ctypes.byref(info))
+    return info
+
+
+def test_decode_plan_keeps_whole_rows_in_short_launches():
+    """The automatic partition keeps whole rows (no merge pass) when the
+    launch is short, whole rows already give every CU an item and no row
+    is longer than two minimum partitions; longer launches keep their
+    splits."""
+    from kunserve_amd import workloads
+    w = workloads.single_layer_decode()       # 8 rows x 32 heads, contexts U[128, 512]
+    info = _auto_decode_plan(w.kv_len, 32, 32)
+    assert info.num_merge == 0 and info.num_work == w.batch and info.part_tokens == 512
+    # fewer row-head items than CUs: rows stay split for parallelism
+    info = _auto_decode_plan(w.kv_len, 32, 32, num_cus=1024)
+    assert info.part_tokens == 256 and info.num_merge > 0
+    # a row longer than two minimum partitions: split
+    info = _auto_decode_plan(np.r_[w.kv_len, 600], 32, 32)
+    assert info.part_tokens == 256 and info.num_merge > 0
+    # the Llama-2-7B and Llama-3-8B GQA workloads keep their partitions
+    w = workloads.llama2_7b_decode()
+    assert _auto_decode_plan(w.kv_len, 32, 32).part_tokens == 512
+    w = workloads.llama3_8b_gqa_decode()
+    assert _auto_decode_plan(w.kv_len, 32, 8).part_tokens == 2048
+
+
 def test_decode_plan_rejects_bad_arguments():
     kv = np.array([10, 20], dtype=np.int32)
     buf = np.zeros(64, dtype=np.int32)
