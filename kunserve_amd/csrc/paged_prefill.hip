@@ -871,42 +871,63 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     step_last(vcur, 1);
     tile_end();
   }
-  for (int it = t_int; it < ntiles; ++it) {
+  // The wave's rows are final after its last visible key: writes them
+  // (normalised, or as split partials).
+  auto finish = [&]() {
+    lsum += __shfl_xor(lsum, 32);
+    if (!row_ok) return;
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    if (slot < 0) {
+      typedef typename Vec<T>::v4 V4;
+      f16* op = a.out + int64_t(qt + qrow) * a.o_tok + int64_t(hq) * a.o_head;
+#pragma unroll
+      for (int dt = 0; dt < G::kBlocks; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const V4 val = {T(o[dt][4 * g] * inv), T(o[dt][4 * g + 1] * inv),
+                          T(o[dt][4 * g + 2] * inv), T(o[dt][4 * g + 3] * inv)};
+          *reinterpret_cast<V4*>(op + 32 * dt + 8 * g + 4 * h) = val;
+        }
+      return;
+    }
+    const int64_t prow = int64_t(slot) * G::kTileQ + (qrow - q0);
+    float* po = a.part_o + prow * D;
+#pragma unroll
+    for (int dt = 0; dt < G::kBlocks; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 val = {o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                           o[dt][4 * g + 3] * inv};
+        *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * g + 4 * h) = val;
+      }
+    if (h == 0) {
+      a.part_ml[2 * prow] = m;
+      a.part_ml[2 * prow + 1] = lsum;
+    }
+  };
+  // Diagonal tiles. A wave writes its rows right after the tile of its last
+  // visible key, before that tile's barrier, and then only passes the
+  // remaining barriers: its stores drain while the waves with more diagonal
+  // half-steps (rows further down) still compute. Writing every wave's rows
+  // after the last barrier left a workgroup's output (64 KiB at head_dim
+  // 128) to drain with its CU otherwise idle, about 4% of the chunked-prefill
+  // workload's time.
+  const int it_last = min(ntiles - 1, j_last >> 1);   // uniform; < t_int: no visible key here
+  int it = t_int;
+  for (; it < it_last; ++it) {
     half_masked(kcur, vcur, 2 * it);
     half_masked(kcur, vcur, 2 * it + 1);
     __syncthreads();
     tile_end();
   }
-
-  lsum += __shfl_xor(lsum, 32);
-  if (!row_ok) return;
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  if (slot < 0) {
-    typedef typename Vec<T>::v4 V4;
-    f16* op = a.out + int64_t(qt + qrow) * a.o_tok + int64_t(hq) * a.o_head;
-#pragma unroll
-    for (int dt = 0; dt < G::kBlocks; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const V4 val = {T(o[dt][4 * g] * inv), T(o[dt][4 * g + 1] * inv),
-                        T(o[dt][4 * g + 2] * inv), T(o[dt][4 * g + 3] * inv)};
-        *reinterpret_cast<V4*>(op + 32 * dt + 8 * g + 4 * h) = val;
-      }
-    return;
+  if (it == it_last) {
+    half_masked(kcur, vcur, 2 * it);
+    half_masked(kcur, vcur, 2 * it + 1);
   }
-  const int64_t prow = int64_t(slot) * G::kTileQ + (qrow - q0);
-  float* po = a.part_o + prow * D;
-#pragma unroll
-  for (int dt = 0; dt < G::kBlocks; ++dt)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 val = {o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
-                         o[dt][4 * g + 3] * inv};
-      *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * g + 4 * h) = val;
-    }
-  if (h == 0) {
-    a.part_ml[2 * prow] = m;
-    a.part_ml[2 * prow + 1] = lsum;
+  finish();
+  for (; it < ntiles; ++it) {   // the barrier of tile it_last, then those of the later tiles
+    __syncthreads();
+    tile_end();
   }
 }
 
