@@ -1525,6 +1525,34 @@ extern "C" int kunserve_prefill_plan(const int32_t* q_indptr_host, const int32_t
       }
     }
   }
+  // Each XCD's workgroups in decreasing estimated duration (longest
+  // processing time first: the XCD's CUs take them in this order as they
+  // free up), interior KV tiles counting 1, diagonal tiles 1.6 and a
+  // workgroup's start 3.5 (the kernel's measured per-tile and start-up
+  // times). Ordering groups by their total left a step's single-tile items
+  // (last chunks) behind cheaper tiles of longer groups, and the steps with
+  // 1-3 workgroups per CU ended on them (chunked-prefill workload: +1-3%).
+  for (auto& l : lanes) {
+    const size_t n = l.size() / kRec;
+    std::vector<std::pair<double, size_t>> order(n);
+    for (size_t i = 0; i < n; ++i) {
+      const int32_t* r = l.data() + kRec * i;
+      const int32_t ql = q_indptr_host[r[0] + 1] - q_indptr_host[r[0]];
+      const int32_t prefix = kv_len_host[r[0]] - ql;
+      const int32_t t_lo = r[3] / kTileKV, t_hi = (r[4] + kTileKV - 1) / kTileKV;
+      const int32_t t_int = std::max(t_lo, std::min(t_hi, (prefix + r[1] + 1) / kTileKV));
+      order[i] = {3.5 + (t_int - t_lo) + 1.6 * (t_hi - t_int), i};
+    }
+    std::stable_sort(order.begin(), order.end(),
+                     [](const std::pair<double, size_t>& a, const std::pair<double, size_t>& b) {
+                       return a.first > b.first;
+                     });
+    std::vector<int32_t> sorted(l.size());
+    for (size_t i = 0; i < n; ++i)
+      std::copy(l.begin() + kRec * order[i].second, l.begin() + kRec * (order[i].second + 1),
+                sorted.begin() + kRec * i);
+    l.swap(sorted);
+  }
   size_t depth = 0;
   for (const auto& l : lanes) depth = std::max(depth, l.size() / kRec);
   const int64_t need = int64_t(kRec) * int64_t(depth) * kXcds + int64_t(merges.size());
