@@ -13,8 +13,9 @@ sequences, prompts U[512, 4096], prefixes U[0, 2048], chunk 512) as MFMA
 utilisation of the fp16 dense peak (and `prefill_page256`, the same
 workload on 256-token pages, the reference's default block size, and
 `bf16_prefill_page256` on a bf16 pool of 256-token pages, both reference
-defaults), beside `mfma_ceiling`, the rate the part sustains on fp16 MFMAs
-with random and with constant operands;
+defaults; `prefill_head_dim64` and `prefill_head_dim256`, the same rows and
+heads at head_dim 64 and 256, attention only), beside `mfma_ceiling`, the
+rate the part sustains on fp16 MFMAs with random and with constant operands;
 `gqa_decode` — Llama-3-8B GQA decode (32/8 heads, batch 128, contexts
 U[1024, 8192]) as HBM bandwidth; `bf16_decode` — the headline decode on a
 bf16 pool (the reference's default dtype), and `bf16_decode_page256` on a
@@ -724,11 +725,18 @@ def cpu_decode_sample(w, pool, layer, q, rows, budget_s: float) -> dict:
 # ----------------------------------------------------------------- prefill
 
 
-def bench_prefill(args, device, page_size=16, dtype=torch.float16):
+def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None):
+    """The chunked-prefill workload's 8 steps. head_dim (64 or 256) runs the
+    same rows, pages and heads at another head size: attention only."""
+    import dataclasses
+
     import kunserve_amd as ks
     from kunserve_amd import workloads
 
     w = workloads.chunked_prefill(page_size=page_size)
+    full = head_dim is None
+    if not full:
+        w = dataclasses.replace(w, head_dim=head_dim, name=f"{w.name} head_dim{head_dim}")
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed)
     pool = ks.KVPool.allocate(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device,
@@ -779,7 +787,7 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16):
             ks.append_kv(pool, 0, table, qi, k, v)
 
     rope = append = None
-    if page_size == 16 and dtype == torch.float16:
+    if page_size == 16 and dtype == torch.float16 and full:
         run_rope()
         run_append()
         reps_bw = 8
@@ -847,18 +855,20 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16):
         nbytes += 2 * T * w.num_qo_heads * w.head_dim * elem
         nbytes += int(((kv + w.page_size - 1) // w.page_size).sum()) * 4
     roof_ms = max(flops / (FP16_MFMA_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
-    log(f"prefill ({name}, page {page_size}): {len(steps)} chunk steps, {elapsed * 1e3:.3f} ms with "
+    log(f"prefill ({name}, page {page_size}, head_dim {w.head_dim}): {len(steps)} chunk steps, "
+        f"{elapsed * 1e3:.3f} ms with "
         f"append; attention {attn_ms:.3f} ms = {tflops:.1f} TFLOP/s "
         f"({tflops / FP16_MFMA_PEAK_TFLOPS * 100:.1f}% of the {name} MFMA peak)")
     cpu = None
-    if page_size == 16 and dtype == torch.float16 and not args.no_cpu_baseline:
+    if page_size == 16 and dtype == torch.float16 and full and not args.no_cpu_baseline:
         cpu = cpu_prefill_sample(w, pool, steps[0], args.cpu_budget / 4)
         log(f"prefill cpu baseline: {cpu['value']:.4f} TFLOP/s ({cpu['sample']})")
     log(f"prefill ({name}, page {page_size}): {nbytes / 1e9:.2f} GB algorithmic, "
         f"{flops / nbytes:.0f} flop/B against a ridge of "
         f"{FP16_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):.0f}; roofline time "
         f"{roof_ms:.3f} ms = {roof_ms / attn_ms * 100:.1f}% of the measured")
-    return {"workload": w.name, "dtype": name, "causal_tflop": flops / 1e12, "steps": len(steps),
+    return {"workload": w.name, "dtype": name, "head_dim": w.head_dim,
+            "causal_tflop": flops / 1e12, "steps": len(steps),
             "ms_with_append": elapsed * 1e3, "attention_ms": attn_ms, "tflops": tflops,
             "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS, "page_size": page_size,
             "algorithmic_bytes": nbytes, "flop_per_byte": flops / nbytes,
@@ -1030,7 +1040,7 @@ def main():
     ap.add_argument("--part-tokens", type=int, default=0, help="decode partition (0 = auto)")
     ap.add_argument("--only", choices=["decode", "prefill", "prefill256", "gqa", "bf16",
                                        "bf16p256", "bf16prefill", "remap", "pmm", "swap",
-                                       "mfma", "single", "mixed"],
+                                       "mfma", "single", "mixed", "prefillhd"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
@@ -1066,6 +1076,10 @@ def main():
         return
     if args.only == "mfma":
         print(json.dumps({"mfma_ceiling": mfma_ceiling(device)}))
+        return
+    if args.only == "prefillhd":
+        print(json.dumps({f"prefill_head_dim{hd}": bench_prefill(args, device, head_dim=hd)
+                          for hd in (64, 256)}))
         return
     if args.only == "prefill256":
         print(json.dumps({"prefill_page256": bench_prefill(args, device, page_size=256)}))
@@ -1105,6 +1119,7 @@ def main():
     torch.cuda.empty_cache()
     prefill = prefill256 = prefill_bf16 = gqa = bf16 = bf16_256 = remap = pmm = swp = None
     ceiling = single = mixed = None
+    prefill_hd = {"prefill_head_dim64": None, "prefill_head_dim256": None}
     if args.only is None:
         single = bench_single_layer(args, device)
         torch.cuda.empty_cache()
@@ -1119,6 +1134,13 @@ def main():
         torch.cuda.empty_cache()
         prefill_bf16 = bench_prefill(args, device, page_size=256, dtype=torch.bfloat16)
         torch.cuda.empty_cache()
+        prefill_hd = {}
+        for hd in (64, 256):
+            r = bench_prefill(args, device, head_dim=hd)
+            prefill_hd[f"prefill_head_dim{hd}"] = {
+                k: r[k] for k in ("workload", "head_dim", "causal_tflop", "attention_ms", "tflops",
+                                  "mfma_util")}
+            torch.cuda.empty_cache()
         gqa = bench_gqa(args, device)
         torch.cuda.empty_cache()
         bf16 = bench_bf16_decode(args, device)
@@ -1170,6 +1192,7 @@ def main():
         "prefill": prefill,
         "mfma_ceiling": ceiling,
         "prefill_page256": prefill256,
+        **prefill_hd,
         "gqa_decode": gqa,
         "bf16_decode": bf16,
         "bf16_decode_page256": bf16_256,
