@@ -752,7 +752,8 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None
         T = int(q_indptr[-1])
         table = ks.PageTable(indptr, indices, kv, device)
         qi = torch.from_numpy(q_indptr).to(device)
-        plan = ks.PrefillPlan(q_indptr, kv, w.num_qo_heads, w.num_kv_heads, device)
+        plan = ks.PrefillPlan(q_indptr, kv, w.num_qo_heads, w.num_kv_heads, device,
+                              head_dim=w.head_dim)
         mk = lambda h: torch.randn((T, h, w.head_dim), generator=gen, device=device).to(dtype)
         steps.append((table, qi, plan, mk(w.num_qo_heads), mk(w.num_kv_heads),
                       mk(w.num_kv_heads), torch.empty((T, w.num_qo_heads, w.head_dim),
