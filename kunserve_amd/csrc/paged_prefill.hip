@@ -259,6 +259,14 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
     const f16* qp = a.q + int64_t(qt + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
+    // The running max is folded into the score MFMAs: q is scaled by
+    // scale * log2(e) (rounded once, from the fp32 product) and each score
+    // chain starts from cm = -m, so a probability is exp2 of the MFMA's
+    // result, with no per-score FMA.
+#pragma unroll
+    for (int s = 0; s < G::kSteps; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] = T(float(qf[s][e]) * a.scale_log2);
   }
 
   // Stage (or, for rows with too many pages, only scan) the page ids of
@@ -292,7 +300,11 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   f32x16 o[G::kBlocks];
 #pragma unroll
   for (int i = 0; i < G::kBlocks; ++i) o[i] = f32x16{};
-  float m = -1.0e30f;   // running max of this row, in scaled (log2) units
+  // Running max of this row in log2 units; kNoMax until the row has seen a
+  // key (the score chains then start from 0 and yield absolute scores).
+  constexpr float kNoMax = -1.0e30f;
+  float m = kNoMax;
+  f32x16 cm = {};
   float lsum = 0.f;     // this lane's share of the row sum (other half: lane ^ 32)
 
   const f16* kbase = a.k + int64_t(hkv) * a.head_stride;
@@ -368,7 +380,7 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
     f32x16 st[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      st[mt] = mfma32(*reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch), qf[0], f32x16{});
+      st[mt] = mfma32(*reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch), qf[0], cm);
 #pragma unroll
       for (int s = 1; s < G::kSteps; ++s) {
         const V8 ka = *reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch + 16 * s);
@@ -399,18 +411,29 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
 #pragma unroll
         for (int v = 0; v < 16; ++v) mx = fmaxf(mx, st[mt][v]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
-    // Lazy running max: move it only when the tile's max exceeds it by more
-    // than 8 (log2 units). Probabilities then stay <= 2^8, far inside the
-    // fp16 range, and the O rescale is skipped unless some row of the wave
-    // moved.
-    if (__any(mx > m + 8.f)) {
-      const float m_new = mx > m + 8.f ? mx : m;
-      const float alpha = fast_exp2(m - m_new);
-      m = m_new;
-      lsum *= alpha;
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // Lazy running max: move it only when the tile's max (relative to m)
+    // exceeds 8 (log2 units). Probabilities then stay <= 2^8, far inside
+    // the fp16 range, and the O rescale is skipped unless some row of the
+    // wave moved. A move also shifts this tile's scores and cm.
+    {
+      const bool fresh = m == kNoMax;
+      const bool move = fresh ? mx > -INFINITY : mx > 8.f;
+      if (__any(move)) {
+        const float shift = move ? mx : 0.f;
+        const float alpha = fresh ? 1.f : fast_exp2(-shift);
+        m = move ? (fresh ? mx : m + mx) : m;
+        lsum *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < G::kBlocks; ++dt) o[dt] *= alpha;
+        for (int dt = 0; dt < G::kBlocks; ++dt) o[dt] *= alpha;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) st[mt][v] -= shift;
+        const float c = m == kNoMax ? 0.f : -m;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) cm[v] = c;
+      }
     }
 
     // P^T as B operands: k-step ks covers tokens 16ks + 4h + {0..3} and
@@ -421,7 +444,7 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float p = fast_exp2(fmaf(st[mt][v], a.scale_log2, -m));
+        const float p = fast_exp2(st[mt][v]);
         ps += p;
         pb[2 * mt + (v >> 3)][v & 7] = T(p);
       }
