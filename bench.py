@@ -807,10 +807,29 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None
         run_copy()
         copy_ms = region_ms(lambda: [run_copy() for _ in range(reps_bw)], device) / reps_bw
         del dsts
+        # And this library's copy kernel (the block copy's launch shape), one
+        # launch per step over the step's k and v bytes (rounded down to the
+        # kernel's 256 KiB unit), as the append.
+        from kunserve_amd import _lib
+        step_bytes = [(2 * k.numel() * k.element_size()) // 262144 * 262144
+                      for _, _, _, _, k, v, _ in steps]
+        lib_bytes = 2 * sum(step_bytes)           # read and written
+        src = torch.empty(max(step_bytes), dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        stream = torch.cuda.current_stream(device).cuda_stream
+
+        def run_lib_copy():
+            for nb in step_bytes:
+                _lib.call("kunserve_hbm_probe", 2, src.data_ptr(), dst.data_ptr(), nb, stream)
+        run_lib_copy()
+        lib_copy_ms = region_ms(lambda: [run_lib_copy() for _ in range(reps_bw)], device) / reps_bw
+        del src, dst
         log(f"rope + append prologue: {rope_ms:.3f} ms for the 8 steps = "
             f"{gbs(rope_bytes, rope_ms):.1f} GB/s; append alone {append_ms:.3f} ms = "
             f"{gbs(append_bytes, append_ms):.1f} GB/s; a plain copy of the steps' k and v "
-            f"{copy_ms:.3f} ms = {gbs(append_bytes, copy_ms):.1f} GB/s")
+            f"{copy_ms:.3f} ms = {gbs(append_bytes, copy_ms):.1f} GB/s (torch), "
+            f"{lib_copy_ms:.3f} ms = {gbs(lib_bytes, lib_copy_ms):.1f} GB/s (this library's copy "
+            f"kernel, one launch per step)")
         rope = {"ms": rope_ms, "bytes": rope_bytes, "gbs": gbs(rope_bytes, rope_ms),
                 "hbm_frac": gbs(rope_bytes, rope_ms) / HBM_PEAK_GBS,
                 "launches": len(steps) * reps_bw}
@@ -818,7 +837,9 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None
                   "hbm_frac": gbs(append_bytes, append_ms) / HBM_PEAK_GBS,
                   "launches": len(steps) * reps_bw,
                   "plain_copy_same_bytes_gbs": gbs(append_bytes, copy_ms),
-                  "frac_of_plain_copy": copy_ms / append_ms}
+                  "frac_of_plain_copy": copy_ms / append_ms,
+                  "library_copy_same_bytes_gbs": gbs(lib_bytes, lib_copy_ms),
+                  "frac_of_library_copy": gbs(append_bytes, append_ms) / gbs(lib_bytes, lib_copy_ms)}
 
     reps = max(1, args.steps // 4)
     for _ in range(max(1, args.warmup)):
