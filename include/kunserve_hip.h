@@ -200,7 +200,8 @@ int kunserve_rope_append_kv(const kunserve_kv_pool* pool, int32_t layer,
 /* ---------------------------------------------- decode attention (A4) */
 
 typedef struct {
-  int32_t num_work;      /* decode work items (partitions)                */
+  int32_t num_work;      /* work records: 8 XCD lanes of partitions,
+                            interleaved, padded with seq -1 records      */
   int32_t num_merge;     /* sequences split over more than one partition  */
   int32_t num_slots;     /* partial-result slots used                     */
   int32_t part_tokens;   /* partition length in tokens                    */

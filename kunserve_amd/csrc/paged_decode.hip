@@ -38,6 +38,7 @@ constexpr int kMaxPartTokens = 4096;
 constexpr int kMinPageSize = 4;
 constexpr int kMaxPartPages = kMaxPartTokens / kMinPageSize + 2;
 constexpr int kMinPartTokens = 256;
+constexpr int kXcds = 8;                 // MI355X: workgroup b runs on XCD b % 8
 constexpr float kNegBig = -1.0e30f;      // finite "minus infinity" for running maxima
 
 // Source of the loads of lanes past a partition's end and of bad page ids:
@@ -57,7 +58,7 @@ struct DecodeArgs {
   int32_t page_shift;
   const int32_t* indptr;
   const int32_t* indices;
-  const int32_t* work;      // [num_work][4]: seq, tok_begin, tok_end, slot (-1: direct)
+  const int32_t* work;      // [num_work][4]: seq (-1: padding), tok_begin, tok_end, slot (-1: direct)
   float* part_o;            // [slots][num_qo_heads][D]
   float* part_lse;          // [slots][num_qo_heads]
   int32_t num_qo_heads;
@@ -67,20 +68,19 @@ struct DecodeArgs {
   float scale_log2;         // sm_scale * log2(e)
 };
 
-// Work item and head group of workgroup b. The hardware hands workgroup b
-// to XCD b % 8; XCD x runs every head group of one item of each group of
-// 8 consecutive items of the plan's longest-first order: item 8r + x for
-// even r and 8r + 7 - x for odd r, so no XCD always gets the longest of
-// the 8. The pages an XCD reads at a time are then those of its own few
-// items (measured 1-2% faster than spreading each item's head groups over
-// all XCDs). Returns false for the grid's padding workgroups (the grid is
-// 8 * ceil(items / 8) * head_groups).
+// Work record and head group of workgroup b. The hardware hands workgroup
+// b to XCD b % 8. The plan's records are 8 lanes interleaved (record
+// 8 r + x is entry r of XCD x's lane), and XCD x runs every head group of
+// its lane's entries in order, an entry's head groups back to back, so the
+// pages an XCD reads at a time are those of its own few items (measured
+// 1-2% faster than spreading each item's head groups over all XCDs). A
+// lane's padding records (seq -1) end the workgroup at once.
 __device__ __forceinline__ bool decode_work(const DecodeArgs& a, int& item, int& hg) {
   const int b = int(blockIdx.x);
   const int j = b >> 3;
   const int local = j / a.head_groups;
   hg = j - local * a.head_groups;
-  item = 8 * local + ((local & 1) ? 7 - (b & 7) : (b & 7));
+  item = 8 * local + (b & 7);
   return item < a.num_work;
 }
 
@@ -106,6 +106,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(DecodeArgs a) {
   if (!decode_work(a, item, hg)) return;   // padding workgroup (uniform: no barrier reached)
   const int32_t* w = a.work + 4 * item;
   const int seq = w[0], tb = w[1], te = w[2], slot = w[3];
+  if (seq < 0) return;   // a lane's padding record (uniform: no barrier reached)
   const int tok = a.q_token ? a.q_token[seq] : seq;   // q / out token of the sequence
   const int hq0 = hg * G;
   const int hkv = hq0 / a.ratio;
@@ -321,6 +322,7 @@ void paged_decode_mfma_kernel(DecodeArgs a) {
   if (!decode_work(a, item, hg)) return;   // padding workgroup (uniform: no barrier reached)
   const int32_t* w = a.work + 4 * item;
   const int seq = w[0], tb = w[1], te = w[2], slot = w[3];
+  if (seq < 0) return;   // a lane's padding record (uniform: no barrier reached)
   const int tok = a.q_token ? a.q_token[seq] : seq;   // q / out token of the sequence
   const int hq0 = hg * G;
   const int hkv = hq0 / a.ratio;
@@ -648,7 +650,8 @@ extern "C" int64_t kunserve_decode_plan_bound(const int32_t* kv_len_host, int32_
   int64_t parts = 0;
   for (int32_t b = 0; b < num_seqs; ++b)
     parts += std::max<int64_t>(1, ceil_div(std::max(kv_len_host[b], 0), kMinPartTokens));
-  return 4 * (parts + num_seqs);
+  // work records (8 lanes, each at most every item) and merge records
+  return 4 * (8 * parts + num_seqs);
 }
 
 extern "C" int kunserve_decode_plan(const int32_t* kv_len_host, int32_t num_seqs,
@@ -714,20 +717,43 @@ extern "C" int kunserve_decode_plan(const int32_t* kv_len_host, int32_t num_seqs
   }
   std::stable_sort(items.begin(), items.end(),
                    [](const Item& x, const Item& y) { return (x.e - x.b) > (y.e - y.b); });
-  const int64_t need = 4 * int64_t(items.size()) + int64_t(merges.size());
+  // One lane per XCD, dealt longest first to the lane that would finish it
+  // first at that XCD's streaming rate. On MI355X the odd XCDs stream decode
+  // about 7% slower than the even ones (10.8 against 11.6 tokens per us per
+  // workgroup at the Llama-2-7B shape, the same on every layer and with the
+  // items rotated across XCDs: a property of the XCD, not of the data), so
+  // an even share left them finishing 5-7 us after the even XCDs. A
+  // workgroup's start costs about 32 tokens of streaming.
+  constexpr double kXcdRate[kXcds] = {1.0, 0.93, 1.0, 0.93, 1.0, 0.93, 1.0, 0.93};
+  constexpr double kItemStartTokens = 32.0;
+  std::vector<Item> lanes[kXcds];
+  double load[kXcds] = {};
+  for (const Item& it : items) {
+    const double cost = double(it.e - it.b) + kItemStartTokens;
+    int best = 0;
+    for (int x = 1; x < kXcds; ++x)
+      if ((load[x] + cost) / kXcdRate[x] < (load[best] + cost) / kXcdRate[best]) best = x;
+    lanes[best].push_back(it);
+    load[best] += cost;
+  }
+  size_t depth = 0;
+  for (const auto& l : lanes) depth = std::max(depth, l.size());
+  const int64_t need = 4 * int64_t(kXcds) * int64_t(depth) + int64_t(merges.size());
   if (need > plan_capacity) {
     set_error("plan needs %lld ints, capacity %lld", (long long)need, (long long)plan_capacity);
     return KUNSERVE_ENOSPC;
   }
   int32_t* p = plan_host;
-  for (const Item& it : items) {
-    *p++ = it.seq;
-    *p++ = it.b;
-    *p++ = it.e;
-    *p++ = it.slot;
-  }
+  for (size_t r = 0; r < depth; ++r)
+    for (int x = 0; x < kXcds; ++x) {
+      const Item it = r < lanes[x].size() ? lanes[x][r] : Item{-1, 0, 0, -1};
+      *p++ = it.seq;
+      *p++ = it.b;
+      *p++ = it.e;
+      *p++ = it.slot;
+    }
   std::copy(merges.begin(), merges.end(), p);
-  info->num_work = int32_t(items.size());
+  info->num_work = int32_t(kXcds * depth);
   info->num_merge = int32_t(merges.size() / 4);
   info->num_slots = slots;
   info->part_tokens = part_tokens;
@@ -802,10 +828,10 @@ extern "C" int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer
   a.scale_log2 = sm_scale * 1.4426950408889634f;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // One dimension, mapped to (item, head group) by decode_work: on every XCD
-  // the dispatch order is the plan's longest-first item order (a launch ends
-  // on its shortest items), with an item's head groups, which read the same
-  // pages, back to back.
+  // One dimension, mapped to (record, head group) by decode_work: on every
+  // XCD the dispatch order is its lane's longest-first order (a launch ends
+  // on short items), with an item's head groups, which read the same pages,
+  // back to back.
   a.head_groups = num_qo_heads / info->group_size;
   a.num_work = info->num_work;
   const int64_t nblocks = 8 * ceil_div(info->num_work, 8) * a.head_groups;

@@ -43,12 +43,10 @@ def test_decode_plan_covers_every_token_once():
         info = _lib.DecodePlanInfo()
         _lib.call("kunserve_decode_plan", kv.ctypes.data, kv.size, hq, hkv, 256, 0,
                   buf.ctypes.data, cap, ctypes.byref(info))
-        work = buf[:4 * info.num_work].reshape(-1, 4)
+        work = _check_lanes(buf[:4 * info.num_work].reshape(-1, 4))
         merges = buf[4 * info.num_work:info.plan_ints].reshape(-1, 4)
         assert info.group_size in (1, 2, 4, 8) and (hq // hkv) % info.group_size == 0
         covered = np.zeros(kv.size, dtype=np.int64)
-        lengths = work[:, 2] - work[:, 1]
-        assert np.all(np.diff(lengths) <= 0), "work is ordered longest first"
         for seq, b, e, slot in work:
             assert 0 <= b <= e <= kv[seq] and e - b <= info.part_tokens
             covered[seq] += e - b
@@ -59,6 +57,39 @@ def test_decode_plan_covers_every_token_once():
             assert n > 1 and set(work[work[:, 0] == seq, 3]) == set(range(s0, s0 + n))
         single = [s for s in range(kv.size) if s not in set(merges[:, 0])]
         assert all((work[work[:, 0] == s, 3] == -1).all() for s in single)
+
+
+def _check_lanes(records):
+    """The decode plan's records are 8 XCD lanes interleaved (record 8 r + x
+    is entry r of lane x): each lane's items come longest first, then only
+    padding (seq -1). Returns the items."""
+    assert records.shape[0] % 8 == 0
+    for x in range(8):
+        lane = records[x::8]
+        real = lane[:, 0] >= 0
+        n = int(real.sum())
+        assert real[:n].all() and not real[n:].any(), "padding only at a lane's end"
+        lengths = lane[:n, 2] - lane[:n, 1]
+        assert np.all(np.diff(lengths) <= 0), "a lane is ordered longest first"
+    return records[records[:, 0] >= 0]
+
+
+def test_decode_plan_weights_odd_xcds():
+    """Lanes are dealt longest first to the XCD that would finish the item
+    first, the odd XCDs at 0.93 of the even ones' rate: with equal items the
+    odd lanes get fewer, and the weighted loads end within one item."""
+    kv = np.full(512, 512, dtype=np.int32)
+    cap = _lib.lib().kunserve_decode_plan_bound(kv.ctypes.data, kv.size)
+    buf = np.zeros(cap, dtype=np.int32)
+    info = _lib.DecodePlanInfo()
+    _lib.call("kunserve_decode_plan", kv.ctypes.data, kv.size, 32, 32, 256, 512,
+              buf.ctypes.data, cap, ctypes.byref(info))
+    rec = buf[:4 * info.num_work].reshape(-1, 4)
+    counts = [int((rec[x::8, 0] >= 0).sum()) for x in range(8)]
+    assert sum(counts) == 512
+    assert min(counts[0::2]) > max(counts[1::2]), counts
+    finish = [counts[x] * (512 + 32) / (1.0 if x % 2 == 0 else 0.93) for x in range(8)]
+    assert max(finish) - min(finish) <= (512 + 32) / 0.93
 
 
 def _auto_decode_plan(kv, hq, hkv, num_cus=256):
@@ -79,7 +110,7 @@ def test_decode_plan_keeps_whole_rows_in_short_launches():
     from kunserve_amd import workloads
     w = workloads.single_layer_decode()       # 8 rows x 32 heads, contexts U[128, 512]
     info = _auto_decode_plan(w.kv_len, 32, 32)
-    assert info.num_merge == 0 and info.num_work == w.batch and info.part_tokens == 512
+    assert info.num_merge == 0 and info.num_work == 8 and info.part_tokens == 512
     # fewer row-head items than CUs: rows stay split for parallelism
     info = _auto_decode_plan(w.kv_len, 32, 32, num_cus=1024)
     assert info.part_tokens == 256 and info.num_merge > 0
@@ -256,7 +287,7 @@ def test_decode_plan_properties(kv, heads, num_cus, part):
     info = _lib.DecodePlanInfo()
     _lib.call("kunserve_decode_plan", kv.ctypes.data if kv.size else None, kv.size, hq, hkv,
               num_cus, part, buf.ctypes.data, cap, ctypes.byref(info))
-    work = buf[:4 * info.num_work].reshape(-1, 4)
+    work = _check_lanes(buf[:4 * info.num_work].reshape(-1, 4))
     merges = buf[4 * info.num_work:info.plan_ints].reshape(-1, 4)
     assert part == 0 or info.part_tokens == part
     covered = np.zeros(kv.size, dtype=np.int64)
@@ -264,7 +295,6 @@ def test_decode_plan_properties(kv, heads, num_cus, part):
         assert 0 <= b <= e <= kv[seq] and e - b <= info.part_tokens
         covered[seq] += e - b
     assert np.array_equal(covered, kv)
-    assert np.all(np.diff(work[:, 2] - work[:, 1]) <= 0)
     assert sorted(work[work[:, 3] >= 0, 3].tolist()) == list(range(info.num_slots))
     for seq, s0, n, _ in merges:
         assert n > 1 and sorted(work[work[:, 0] == seq, 3].tolist()) == list(range(s0, s0 + n))
