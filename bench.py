@@ -161,7 +161,7 @@ def bench_decode(args, device):
     fill_random_(pool.v, gen)
     res = measure_decode(w, pool, list(range(w.num_layers)), args, device)
     plan = res["plan"]
-    log(f"plan: {plan.info.num_work} work items x {w.num_qo_heads // plan.info.group_size} "
+    log(f"plan: {plan.num_items} work items x {w.num_qo_heads // plan.info.group_size} "
         f"head groups, part_tokens {plan.info.part_tokens}, {plan.info.num_merge} merged rows")
     log(f"decode: {res['ms_per_step']:.3f} ms/step, {res['value']:.1f} GB/s whole-step; "
         f"per launch {res['launch_ms'] * 1e3:.1f} us = {res['achieved']:.1f} GB/s "

@@ -354,6 +354,11 @@ class DecodePlan:
     def host_arrays(self) -> list:
         return [self.plan_host]
 
+    @property
+    def num_items(self) -> int:
+        """Work items (partitions) of the plan, without the lanes' padding."""
+        return int((self.plan_host[: 4 * self.info.num_work: 4] >= 0).sum())
+
     def bind(self, dev: Sequence[torch.Tensor]) -> None:
         self.plan = dev[0] if self.info.plan_ints else None
 
