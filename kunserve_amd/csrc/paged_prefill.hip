@@ -259,14 +259,6 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
     const f16* qp = a.q + int64_t(qt + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
-    // The running max is folded into the score MFMAs: q is scaled by
-    // scale * log2(e) (rounded once, from the fp32 product) and each score
-    // chain starts from cm = -m, so a probability is exp2 of the MFMA's
-    // result, with no per-score FMA.
-#pragma unroll
-    for (int s = 0; s < G::kSteps; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[s][e] = T(float(qf[s][e]) * a.scale_log2);
   }
 
   // Stage (or, for rows with too many pages, only scan) the page ids of
@@ -300,11 +292,7 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   f32x16 o[G::kBlocks];
 #pragma unroll
   for (int i = 0; i < G::kBlocks; ++i) o[i] = f32x16{};
-  // Running max of this row in log2 units; kNoMax until the row has seen a
-  // key (the score chains then start from 0 and yield absolute scores).
-  constexpr float kNoMax = -1.0e30f;
-  float m = kNoMax;
-  f32x16 cm = {};
+  float m = -1.0e30f;   // running max of this row, in scaled (log2) units
   float lsum = 0.f;     // this lane's share of the row sum (other half: lane ^ 32)
 
   const f16* kbase = a.k + int64_t(hkv) * a.head_stride;
@@ -380,7 +368,7 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
     f32x16 st[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      st[mt] = mfma32(*reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch), qf[0], cm);
+      st[mt] = mfma32(*reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch), qf[0], f32x16{});
 #pragma unroll
       for (int s = 1; s < G::kSteps; ++s) {
         const V8 ka = *reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch + 16 * s);
@@ -411,29 +399,18 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
 #pragma unroll
         for (int v = 0; v < 16; ++v) mx = fmaxf(mx, st[mt][v]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // Lazy running max: move it only when the tile's max (relative to m)
-    // exceeds 8 (log2 units). Probabilities then stay <= 2^8, far inside
-    // the fp16 range, and the O rescale is skipped unless some row of the
-    // wave moved. A move also shifts this tile's scores and cm.
-    {
-      const bool fresh = m == kNoMax;
-      const bool move = fresh ? mx > -INFINITY : mx > 8.f;
-      if (__any(move)) {
-        const float shift = move ? mx : 0.f;
-        const float alpha = fresh ? 1.f : fast_exp2(-shift);
-        m = move ? (fresh ? mx : m + mx) : m;
-        lsum *= alpha;
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
+    // Lazy running max: move it only when the tile's max exceeds it by more
+    // than 8 (log2 units). Probabilities then stay <= 2^8, far inside the
+    // fp16 range, and the O rescale is skipped unless some row of the wave
+    // moved.
+    if (__any(mx > m + 8.f)) {
+      const float m_new = mx > m + 8.f ? mx : m;
+      const float alpha = fast_exp2(m - m_new);
+      m = m_new;
+      lsum *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < G::kBlocks; ++dt) o[dt] *= alpha;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) st[mt][v] -= shift;
-        const float c = m == kNoMax ? 0.f : -m;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) cm[v] = c;
-      }
+      for (int dt = 0; dt < G::kBlocks; ++dt) o[dt] *= alpha;
     }
 
     // P^T as B operands: k-step ks covers tokens 16ks + 4h + {0..3} and
@@ -444,7 +421,7 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float p = fast_exp2(st[mt][v]);
+        const float p = fast_exp2(fmaf(st[mt][v], a.scale_log2, -m));
         ps += p;
         pb[2 * mt + (v >> 3)][v & 7] = T(p);
       }
@@ -739,13 +716,6 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     for (int wv = 0; wv < G::kComputeWaves; ++wv) bad |= s_bad[wv];
     any_bad = __builtin_amdgcn_readfirstlane(bad) != 0;
   }
-  // At head_dim 64 the running max is folded into the score MFMAs: q is
-  // scaled by scale * log2(e) once, the score chain starts from cm = -m
-  // instead of zero, and a probability is exp2 of the MFMA's result, with no
-  // per-score FMA. At 128 the 16 registers of cm do not fit beside the
-  // pipeline (three waves per SIMD allow 168), so scores are scaled and
-  // shifted per score.
-  constexpr bool kFold = D == 64;
   // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8
   // (a row past q_len reads the sequence's first row and writes nothing).
   V8 qf[G::kSteps];
@@ -753,23 +723,12 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     const f16* qp = a.q + int64_t(qt + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
 #pragma unroll
     for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
-    if constexpr (kFold) {
-      // rounded once, from the fp32 product
-#pragma unroll
-      for (int s = 0; s < G::kSteps; ++s)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[s][e] = T(float(qf[s][e]) * a.scale_log2);
-    }
   }
   const int qpos = prefix + qrow;
   f32x16 o[G::kBlocks];
 #pragma unroll
   for (int i = 0; i < G::kBlocks; ++i) o[i] = f32x16{};
-  // Running max of this row in log2 units; kNoMax until the row has seen a
-  // key. Folded: the score chain starts from cm = -m (0 while kNoMax).
-  constexpr float kNoMax = -1.0e30f;
-  float m = kNoMax;
-  f32x16 cm = {};
+  float m = -1.0e30f;   // running max of this row, in log2 units
   float lsum = 0.f;     // this lane's share of the row sum (other half: lane ^ 32)
   V8 ones;
 #pragma unroll
@@ -782,44 +741,25 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
   // (r, h) holds tokens 32 j + 8 (v / 4) + 4 h + v % 4 of row r.
   auto half_scores = [&](int kbuf, int hh) {
     const T* kt = sK + kbuf * G::kKHalves + kb0 + 32 * hh * G::kKPitch;
-    f32x16 s = mfma32(*reinterpret_cast<const V8*>(kt), qf[0], kFold ? cm : f32x16{});
+    f32x16 s = mfma32(*reinterpret_cast<const V8*>(kt), qf[0], f32x16{});
 #pragma unroll
     for (int st = 1; st < G::kSteps; ++st)
       s = mfma32(*reinterpret_cast<const V8*>(kt + 16 * st), qf[st], s);
     return s;
   };
-  // Row max in log2 units (lanes r and r + 32 hold the two halves of row r);
-  // folded, relative to m (absolute while m is kNoMax).
+  // Row max in log2 units (lanes r and r + 32 hold the two halves of row r).
   auto row_max = [&](const f32x16& s) {
     float mx = -INFINITY;
 #pragma unroll
     for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
     const auto sw = __builtin_amdgcn_permlane32_swap(f32_to_bits(mx), f32_to_bits(mx), false, false);
-    const float r = fmaxf(bits_to_f32(sw[0]), bits_to_f32(sw[1]));
-    return kFold ? r : r * a.scale_log2;
+    return fmaxf(bits_to_f32(sw[0]), bits_to_f32(sw[1])) * a.scale_log2;
   };
   // Lazy running max: moved only when a row's max exceeds it by more than
   // 8 (log2 units), so probabilities stay <= 2^8 (far inside the fp16
   // range), and the O rescale is skipped unless some row of the wave moved.
-  // Folded, the move also shifts the half-step's scores sv and cm.
-  auto rescale = [&](f32x16& sv, float mx) {
-    if constexpr (kFold) {
-      const bool fresh = m == kNoMax;
-      const bool move = fresh ? mx > -INFINITY : mx > 8.f;
-      if (__any(move)) {
-        const float shift = move ? mx : 0.f;
-        const float alpha = fresh ? 1.f : fast_exp2(-shift);
-        m = move ? (fresh ? mx : m + mx) : m;
-        lsum *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < G::kBlocks; ++dt) o[dt] *= alpha;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) sv[v] -= shift;
-        const float c = m == kNoMax ? 0.f : -m;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) cm[v] = c;
-      }
-    } else if (__any(mx > m + 8.f)) {
+  auto rescale = [&](float mx) {
+    if (__any(mx > m + 8.f)) {
       const float m_new = mx > m + 8.f ? mx : m;
       const float alpha = fast_exp2(m - m_new);
       m = m_new;
@@ -833,8 +773,7 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
   // taken over the rounded probabilities the P.V product uses.
   auto probs = [&](const f32x16& s, V8 (&pb)[2]) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v)
-      pb[v >> 3][v & 7] = T(fast_exp2(kFold ? s[v] : fmaf(s[v], a.scale_log2, -m)));
+    for (int v = 0; v < 16; ++v) pb[v >> 3][v & 7] = T(fast_exp2(fmaf(s[v], a.scale_log2, -m)));
     lsum = dot8(pb[0], ones, lsum);
     lsum = dot8(pb[1], ones, lsum);
   };
@@ -865,7 +804,7 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     pv(vbuf, hh, pb);
     const float mx = row_max(sn);
     sc = sn;
-    rescale(sc, mx);
+    rescale(mx);
   };
   auto step_last = [&](int vbuf, int hh) {
     V8 pb[2];
@@ -898,7 +837,7 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     if (j > j_last) return;   // uniform per wave
     f32x16 sv = half_scores(kbuf, j & 1);
     mask(sv, j, kbuf);
-    rescale(sv, row_max(sv));
+    rescale(row_max(sv));
     V8 pb[2];
     probs(sv, pb);
     pv(vbuf, j & 1, pb);
@@ -920,7 +859,7 @@ __global__ __launch_bounds__(WsGeom<D>::kThreads) void paged_prefill_ws_kernel(P
     }
   } else if (t_int > t_first) {
     sc = half_scores(0, 0);
-    rescale(sc, row_max(sc));
+    rescale(row_max(sc));
     for (int it = t_first; it + 1 < t_int; ++it) {
       step(kcur, 1, vcur, 0);
       __syncthreads();
