@@ -44,6 +44,26 @@ def test_single_layer_decode_b8(device):
 
 
 @pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 4), (64, 8)])
+def test_decode_large_scores_match_oracle(device, head_dim, hq, hkv):
+    """q ~ N(0, 8^2): scores span tens of log2 units (sharp softmax, many
+    moves of the running max, split rows merged by log-sum-exp); the VALU
+    kernel (group 1) and the MFMA kernel (groups 4, 8) keep fp32 scores."""
+    rng = np.random.default_rng(head_dim + hq)
+    ps, npg = 16, 400
+    kv = np.array([3, 64, 300, 1000, 2500], dtype=np.int32)
+    need = (kv + ps - 1) // ps
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, hkv, ps, head_dim, device, 23)
+    pool.v.mul_(0.5)
+    q, out, plan = run_decode(pool, 0, indptr, indices, kv, hq, device, 24, 256, 8.0)
+    assert plan.info.num_merge > 0
+    want = oracle_decode(pool, 0, indptr, indices, kv, q)
+    assert max_abs(out, want) <= ATOL
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
 @pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (16, 2), (16, 1), (12, 4), (64, 8)])
 def test_decode_heads_and_dims(device, head_dim, hq, hkv):
     rng = np.random.default_rng(hq * 1000 + hkv * 10 + head_dim)
