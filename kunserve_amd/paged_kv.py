@@ -66,6 +66,9 @@ def _upload_packed(arrays: Sequence[np.ndarray], device: torch.device) -> list:
 _DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
 
 
+_V_OFFSET_ELEMS = 2048   # 4 KiB of 16-bit elements
+
+
 class KVPool:
     """Separate K and V pools of shape [num_pages, num_layers, num_kv_heads,
     page_size, head_dim] (any strides with head_dim contiguous), float16 or
@@ -96,8 +99,15 @@ class KVPool:
     def allocate(cls, num_pages: int, num_layers: int, num_kv_heads: int, page_size: int,
                  head_dim: int, device="cuda", dtype: torch.dtype = FP16) -> "KVPool":
         shape = (num_pages, num_layers, num_kv_heads, page_size, head_dim)
+        # V starts 4 KiB into its allocation. Decode loads the K and the V slab
+        # of a (page, layer, head) back to back; offset this way they are
+        # served about 1% faster (Llama-2-7B decode: 142.6-142.7 against
+        # 143.9 us per launch with V at its allocation's start; 1 KiB measured
+        # the same, 256 bytes and 2 KiB in between).
+        n = math.prod(shape)
+        v = torch.empty(n + _V_OFFSET_ELEMS, dtype=dtype, device=device)
         return cls(torch.empty(shape, dtype=dtype, device=device),
-                   torch.empty(shape, dtype=dtype, device=device))
+                   v[_V_OFFSET_ELEMS:].view(shape))
 
     def check_dtype(self, *tensors: torch.Tensor) -> None:
         for t in tensors:
