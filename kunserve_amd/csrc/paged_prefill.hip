@@ -959,24 +959,48 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MergeArgs a) {
     const int row = blockIdx.y * merge_rows(D) + int(threadIdx.x) / (D / 8);
     const int c = int(threadIdx.x) % (D / 8);
     if (q0 + row >= q_len) return;
+    // Splits are read 8 at a time, each batch's loads issued together: a
+    // loop of one split at a time waited a memory round trip per split
+    // (12 us for the chunked-prefill workload's 8-way split step).
+    constexpr int kBatch = 8;
     float mx = -INFINITY;
-    for (int j = 0; j < n; ++j) {
-      const int64_t pr = int64_t(s0 + j) * kTileQ + row;
-      if (a.part_ml[2 * pr + 1] > 0.f) mx = fmaxf(mx, a.part_ml[2 * pr]);
+    for (int j0 = 0; j0 < n; j0 += kBatch) {
+      float mm[kBatch], ll[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t pr = int64_t(s0 + j0 + u) * kTileQ + row;
+        const bool in = j0 + u < n;
+        mm[u] = in ? a.part_ml[2 * pr] : -INFINITY;
+        ll[u] = in ? a.part_ml[2 * pr + 1] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (ll[u] > 0.f) mx = fmaxf(mx, mm[u]);
     }
     float wsum = 0.f, acc[8] = {};
-    for (int j = 0; j < n; ++j) {
-      const int64_t pr = int64_t(s0 + j) * kTileQ + row;
-      const float l = a.part_ml[2 * pr + 1];
-      if (!(l > 0.f)) continue;
-      const float w = fast_exp2(a.part_ml[2 * pr] - mx) * l;
-      wsum += w;
-      const f32x4 x0 = *reinterpret_cast<const f32x4*>(a.part_o + pr * D + 8 * c);
-      const f32x4 x1 = *reinterpret_cast<const f32x4*>(a.part_o + pr * D + 8 * c + 4);
+    for (int j0 = 0; j0 < n; j0 += kBatch) {
+      float mm[kBatch], ll[kBatch];
+      f32x4 x0[kBatch], x1[kBatch];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[e] = fmaf(w, x0[e], acc[e]);
-        acc[4 + e] = fmaf(w, x1[e], acc[4 + e]);
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t pr = int64_t(s0 + j0 + u) * kTileQ + row;
+        const bool in = j0 + u < n;
+        mm[u] = in ? a.part_ml[2 * pr] : 0.f;
+        ll[u] = in ? a.part_ml[2 * pr + 1] : 0.f;
+        x0[u] = in ? *reinterpret_cast<const f32x4*>(a.part_o + pr * D + 8 * c) : f32x4{};
+        x1[u] = in ? *reinterpret_cast<const f32x4*>(a.part_o + pr * D + 8 * c + 4) : f32x4{};
+      }
+      // in split order, as before
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (!(ll[u] > 0.f)) continue;
+        const float w = fast_exp2(mm[u] - mx) * ll[u];
+        wsum += w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] = fmaf(w, x0[u][e], acc[e]);
+          acc[4 + e] = fmaf(w, x1[u][e], acc[4 + e]);
+        }
       }
     }
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
