@@ -5,10 +5,11 @@
 // HBM-bound: every K/V byte of a sequence is read exactly once per layer.
 // Design for gfx950 (wave64, 256 CUs):
 //  * The host plan cuts every sequence into partitions of part_tokens and
-//    orders them longest first; the grid is work items x head groups, each
-//    XCD running all head groups of one item in every 8 (alternating
-//    direction), so mixed context lengths still give an even,
-//    device-filling grid that is dispatched longest item first on every XCD.
+//    deals them, longest first, to 8 XCD lanes by estimated finish time;
+//    the grid is lane entries x head groups, each XCD running all head
+//    groups of one item at a time, so mixed context lengths still give an
+//    even, device-filling grid that is dispatched longest item first on
+//    every XCD.
 //  * A workgroup (4 waves) owns one partition of one KV head and all
 //    `G` query heads that share it (GQA: one KV read serves G heads).
 //  * The partition's slice of the page table is staged in LDS once; after
