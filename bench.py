@@ -160,6 +160,7 @@ def bench_decode(args, device):
     fill_random_(pool.k, gen)
     fill_random_(pool.v, gen)
     res = measure_decode(w, pool, list(range(w.num_layers)), args, device)
+    res["access_pattern"] = slab_ceiling(w, pool, res["plan"], device, res["launch_ms"])
     plan = res["plan"]
     log(f"plan: {plan.num_items} work items x {w.num_qo_heads // plan.info.group_size} "
         f"head groups, part_tokens {plan.info.part_tokens}, {plan.info.num_merge} merged rows")
@@ -167,6 +168,49 @@ def bench_decode(args, device):
         f"per launch {res['launch_ms'] * 1e3:.1f} us = {res['achieved']:.1f} GB/s "
         f"({res['achieved'] / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
     return res
+
+
+def slab_ceiling(w, pool, plan, device, launch_ms, reps=5):
+    """The decode's own access pattern, timed alone: kunserve_decode_slab_probe
+    reads every K/V slab (one page's tokens of one KV head) the launch reads,
+    in the partition kernel's workgroup shape, with the offsets precomputed
+    and no arithmetic, over the same layers. A launch near this time is
+    bound by how its slabs are served, not by its lookups or arithmetic."""
+    from kunserve_amd import _lib
+
+    indptr, indices = w.csr()
+    rec = plan.plan_host[: 4 * plan.info.num_work].reshape(-1, 4)
+    rec = rec[rec[:, 0] >= 0]
+    shift = int(w.page_size).bit_length() - 1
+    max_slabs = max(1, plan.info.part_tokens // w.page_size + 1)
+    es = pool.k.element_size()
+    base = np.zeros((len(rec), max_slabs), dtype=np.int64)
+    counts = np.zeros(len(rec), dtype=np.int32)
+    for i, (seq, tb, te, _) in enumerate(rec):
+        if te > tb:
+            pages = indices[indptr[seq] + (tb >> shift): indptr[seq] + ((te - 1) >> shift) + 1]
+            base[i, : len(pages)] = pages.astype(np.int64) * pool.k.stride(0) * es
+            counts[i] = len(pages)
+    slab_bytes = w.page_size * w.head_dim * es
+    offs = [torch.from_numpy(base + layer * pool.k.stride(1) * es).to(device)
+            for layer in range(w.num_layers)]
+    cnt = torch.from_numpy(counts).to(device)
+    sink = torch.empty(len(rec) * w.num_kv_heads, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+
+    def sweep():
+        for o in offs:
+            _lib.call("kunserve_decode_slab_probe", pool.k.data_ptr(), pool.v.data_ptr(),
+                      o.data_ptr(), cnt.data_ptr(), len(rec), max_slabs,
+                      pool.k.stride(2) * es, w.num_kv_heads, slab_bytes, sink.data_ptr(), stream)
+    sweep()
+    ms = region_ms(lambda: [sweep() for _ in range(reps)], device) / (reps * w.num_layers)
+    nbytes = 2 * slab_bytes * int(counts.sum()) * w.num_kv_heads
+    log(f"decode access pattern alone (slab probe): {ms * 1e3:.1f} us per layer = "
+        f"{nbytes / (ms * 1e-3) / 1e9:.0f} GB/s over {nbytes / 1e6:.0f} MB of slabs; the decode "
+        f"launch takes {launch_ms / ms:.3f}x that")
+    return {"probe_us_per_layer": ms * 1e3, "slab_bytes_per_layer": nbytes,
+            "probe_gbs": nbytes / (ms * 1e-3) / 1e9, "launch_over_probe": launch_ms / ms}
 
 
 def bench_single_layer(args, device):
@@ -1205,6 +1249,7 @@ def main():
             "frac": round(dec["achieved"] / HBM_PEAK_GBS, 4),
             "traffic": load_traffic(),
             "kernel": "paged_decode_kernel<f16, 128, 1> + decode_merge_kernel<f16, 128> (one launch per layer)",
+            "access_pattern_ceiling": dec.get("access_pattern"),
             "algorithmic_bytes_per_launch": dec["bytes_per_layer"],
             "launch_us": round(dec["launch_ms"] * 1e3, 2),
         },

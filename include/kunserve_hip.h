@@ -143,6 +143,21 @@ int64_t kunserve_kv_pack_bytes(const kunserve_kv_pool* pool, int32_t num_layers,
 int kunserve_hbm_probe(int32_t mode, const void* src_dev, void* dst_dev,
                        int64_t bytes, kunserve_stream_t stream);
 
+/* Access-pattern calibration (no reference counterpart): reads a decode
+ * launch's K/V slabs (slab_bytes each: one page's tokens of one head, a
+ * multiple of 1 KiB up to 16 KiB) in the partition kernel's workgroup
+ * shape, with no page-table lookups and no arithmetic. Workgroup
+ * i * num_heads + h reads item i's counts_dev[i] slabs at byte offsets
+ * slab_offsets_dev[i * max_slabs + j] + h * head_stride_bytes from k_dev and
+ * v_dev, and writes the XOR of every 32-bit word it read to sink_dev[i *
+ * num_heads + h]. The benchmark times it beside the decode launch. */
+int kunserve_decode_slab_probe(const void* k_dev, const void* v_dev,
+                               const int64_t* slab_offsets_dev,
+                               const int32_t* counts_dev, int32_t num_items,
+                               int32_t max_slabs, int64_t head_stride_bytes,
+                               int32_t num_heads, int32_t slab_bytes,
+                               uint32_t* sink_dev, kunserve_stream_t stream);
+
 /* ------------------------------------------------------------ swap (A7) */
 
 /* torch.ops.swapping_ops.swap (kunserve/worker.py:646-650,673-681):

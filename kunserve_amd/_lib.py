@@ -71,6 +71,8 @@ SIGNATURES = {
                                     c_void_p, c_int64, c_void_p]),
     "kunserve_kv_pack_bytes": (c_int64, [POINTER(KVPool), c_int32, c_int64]),
     "kunserve_hbm_probe": (c_int, [c_int32, c_void_p, c_void_p, c_int64, c_void_p]),
+    "kunserve_decode_slab_probe": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+                                           c_int64, c_int32, c_int32, c_void_p, c_void_p]),
     "kunserve_mfma_probe": (c_int, [c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "kunserve_swap_blocks": (c_int, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p,
                                      c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),

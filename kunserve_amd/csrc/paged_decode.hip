@@ -844,6 +844,105 @@ extern "C" int kunserve_paged_decode(const kunserve_kv_pool* pool, int32_t layer
   return run_decode<f16>(a, *info, plan_dev, pool->head_dim, num_qo_heads, grid, s);
 }
 
+// ------------------------------------------------ access-pattern calibration
+// kunserve_decode_slab_probe reads a decode launch's K/V slabs (one page's
+// tokens of one head: page_size x head_dim elements, contiguous) in the
+// partition kernel's shape, with the slab offsets precomputed and no
+// arithmetic on the data: workgroup i x heads + h reads item i's slabs of
+// head h, its 4 waves striding them, two slabs in flight per wave, 1 KiB per
+// load instruction, non-temporal. Each workgroup XORs what it read into
+// sink[workgroup], so a test can check the bytes.
+namespace kunserve {
+namespace {
+
+constexpr int kMaxSlabLoads = 16;   // 1 KiB loads per slab and tensor (slabs up to 16 KiB)
+
+template <int NL>
+__device__ __forceinline__ void probe_slab(const char* k, const char* v, int64_t off, int lane,
+                                           u32x4 (&x)[2 * NL]) {
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    x[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(k + off + i * 1024 + lane * 16));
+    x[NL + i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(v + off + i * 1024 + lane * 16));
+  }
+}
+
+template <int NL>
+__global__ __launch_bounds__(kThreads) void decode_slab_probe_kernel(
+    const char* k, const char* v, const int64_t* offs, const int32_t* counts, int max_slabs,
+    int64_t head_bytes, int heads, uint32_t* sink) {
+  __shared__ uint32_t s_x[kWaves];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int item = blockIdx.x / heads, head = blockIdx.x % heads;
+  const int n = counts[item];
+  const int64_t* o = offs + int64_t(item) * max_slabs;
+  const int64_t hoff = int64_t(head) * head_bytes;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  u32x4 a[2 * NL], b[2 * NL];
+  int s = wave;
+  if (s < n) probe_slab<NL>(k, v, o[s] + hoff, lane, a);
+  while (s < n) {
+    const int s2 = s + kWaves;
+    if (s2 < n) probe_slab<NL>(k, v, o[s2] + hoff, lane, b);
+#pragma unroll
+    for (int i = 0; i < 2 * NL; ++i) acc ^= a[i];
+    s = s2;
+    if (s >= n) break;
+    const int s3 = s + kWaves;
+    if (s3 < n) probe_slab<NL>(k, v, o[s3] + hoff, lane, a);
+#pragma unroll
+    for (int i = 0; i < 2 * NL; ++i) acc ^= b[i];
+    s = s3;
+  }
+  uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x ^= uint32_t(__shfl_xor(int(x), off));
+  if (lane == 0) s_x[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) r ^= s_x[w];
+    sink[blockIdx.x] = r;
+  }
+}
+
+}  // namespace
+}  // namespace kunserve
+
+extern "C" int kunserve_decode_slab_probe(const void* k_dev, const void* v_dev,
+                                          const int64_t* slab_offsets_dev,
+                                          const int32_t* counts_dev, int32_t num_items,
+                                          int32_t max_slabs, int64_t head_stride_bytes,
+                                          int32_t num_heads, int32_t slab_bytes,
+                                          uint32_t* sink_dev, kunserve_stream_t stream) {
+  using namespace kunserve;
+  clear_error();
+  KSV_CHECK_ARG(k_dev && v_dev && slab_offsets_dev && counts_dev && sink_dev, "null argument");
+  KSV_CHECK_ARG(aligned16(k_dev) && aligned16(v_dev), "pools must be 16-byte aligned");
+  KSV_CHECK_ARG(num_items >= 0 && max_slabs > 0 && num_heads > 0 && head_stride_bytes >= 0,
+                "bad item, slab or head count");
+  KSV_CHECK_ARG(slab_bytes > 0 && slab_bytes % 1024 == 0 && slab_bytes / 1024 <= kMaxSlabLoads,
+                "slab_bytes %d must be a multiple of 1024 up to %d", slab_bytes,
+                kMaxSlabLoads * 1024);
+  KSV_CHECK_ARG(int64_t(num_items) * num_heads < (int64_t(1) << 31), "too many workgroups");
+  if (num_items == 0) return KUNSERVE_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const char* k = static_cast<const char*>(k_dev);
+  const char* v = static_cast<const char*>(v_dev);
+  const dim3 grid(static_cast<unsigned>(int64_t(num_items) * num_heads));
+  switch (slab_bytes / 1024) {
+    case 1: decode_slab_probe_kernel<1><<<grid, kThreads, 0, s>>>(k, v, slab_offsets_dev, counts_dev, max_slabs, head_stride_bytes, num_heads, sink_dev); break;
+    case 2: decode_slab_probe_kernel<2><<<grid, kThreads, 0, s>>>(k, v, slab_offsets_dev, counts_dev, max_slabs, head_stride_bytes, num_heads, sink_dev); break;
+    case 4: decode_slab_probe_kernel<4><<<grid, kThreads, 0, s>>>(k, v, slab_offsets_dev, counts_dev, max_slabs, head_stride_bytes, num_heads, sink_dev); break;
+    case 8: decode_slab_probe_kernel<8><<<grid, kThreads, 0, s>>>(k, v, slab_offsets_dev, counts_dev, max_slabs, head_stride_bytes, num_heads, sink_dev); break;
+    case 16: decode_slab_probe_kernel<16><<<grid, kThreads, 0, s>>>(k, v, slab_offsets_dev, counts_dev, max_slabs, head_stride_bytes, num_heads, sink_dev); break;
+    default: set_error("slab_bytes %d: 1, 2, 4, 8 or 16 KiB", slab_bytes); return KUNSERVE_EINVAL;
+  }
+  KSV_CHECK_LAUNCH();
+  return KUNSERVE_OK;
+}
+
 // ------------------------------------------------ decode without allocation
 // kunserve_paged_decode_noalloc keeps the split partials in `scratch`, a
 // file-scope device array of kNoAllocScratchBytes that every device the

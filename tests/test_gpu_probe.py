@@ -60,3 +60,50 @@ def test_hbm_probe_copy_is_exact():
     _lib.call("kunserve_hbm_probe", 1, None, dst.data_ptr(), dst.numel(), stream)
     torch.cuda.synchronize()
     assert not torch.equal(src, dst)
+
+
+@pytest.mark.parametrize("page_size,head_dim", [(16, 128), (16, 64), (64, 128)])
+def test_decode_slab_probe_reads_the_slabs(page_size, head_dim):
+    """The slab probe XORs exactly the words of its items' slabs (K and V,
+    every head) into one word per workgroup; bad arguments are rejected."""
+    from kunserve_amd import KVPool
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(page_size + head_dim)
+    pool = KVPool.allocate(40, 2, 3, page_size, head_dim, dev)
+    for t in (pool.k, pool.v):
+        t.copy_(torch.randn(t.shape, generator=g, device=dev))
+    rng = np.random.default_rng(0)
+    counts = np.array([5, 0, 1, 8], dtype=np.int32)
+    max_slabs = 8
+    layer = 1
+    es = pool.k.element_size()
+    pages = np.zeros((4, max_slabs), dtype=np.int64)
+    for i, n in enumerate(counts):
+        pages[i, :n] = rng.choice(40, size=n, replace=False)
+    offs = pages * pool.k.stride(0) * es + layer * pool.k.stride(1) * es
+    slab_bytes = page_size * head_dim * es
+    sink = torch.zeros(4 * 3, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    offs_dev = torch.from_numpy(offs).to(dev)
+    cnt_dev = torch.from_numpy(counts).to(dev)
+    _lib.call("kunserve_decode_slab_probe", pool.k.data_ptr(), pool.v.data_ptr(),
+              offs_dev.data_ptr(), cnt_dev.data_ptr(), 4, max_slabs, pool.k.stride(2) * es, 3,
+              slab_bytes, sink.data_ptr(), stream)
+    torch.cuda.synchronize()
+    kw = pool.k.cpu().numpy().view(np.uint32)
+    vw = pool.v.cpu().numpy().view(np.uint32)
+    want = np.zeros(12, dtype=np.uint32)
+    for i, n in enumerate(counts):
+        for h in range(3):
+            x = np.uint32(0)
+            for p in pages[i, :n]:
+                x ^= np.bitwise_xor.reduce(kw[p, layer, h].reshape(-1))
+                x ^= np.bitwise_xor.reduce(vw[p, layer, h].reshape(-1))
+            want[i * 3 + h] = x
+    assert np.array_equal(sink.cpu().numpy().view(np.uint32), want)
+    with pytest.raises(_lib.KunserveError):
+        _lib.call("kunserve_decode_slab_probe", pool.k.data_ptr(), pool.v.data_ptr(),
+                  offs_dev.data_ptr(), cnt_dev.data_ptr(), 4, max_slabs, 0, 3, 1000,
+                  sink.data_ptr(), stream)
+
