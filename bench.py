@@ -72,6 +72,54 @@ def region_ms(fn, device) -> float:
     return ev0.elapsed_time(ev1)
 
 
+def power_during(fn, device, seconds: float = 4.0):
+    """Socket power and GFX clock (amd-smi, sampled from a thread about every
+    0.3 s) while `fn()` runs back to back for `seconds`; None without
+    amd-smi. The part holds its power limit by lowering the clock, so a
+    kernel's clock under load says how much of the part's clock it keeps."""
+    import re
+    import shutil
+    import subprocess
+    import threading
+
+    if not shutil.which("amd-smi"):
+        return None
+    samples = []
+    stop = threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            try:
+                out = subprocess.run(["amd-smi", "metric", "-g", "0", "-p", "-c"],
+                                     capture_output=True, text=True, timeout=10).stdout
+            except (OSError, subprocess.SubprocessError):
+                return
+            pw = re.search(r"SOCKET_POWER:\s*(\d+)", out)
+            clk = [int(x) for x in re.findall(r"GFX_\d+:\s+CLK:\s*(\d+) MHz", out)]
+            if pw and clk:
+                samples.append((int(pw.group(1)), float(np.median(clk))))
+            stop.wait(0.3)
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 1.0:   # reach the steady clock before sampling
+        fn()
+        torch.cuda.synchronize()
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        fn()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join(timeout=15)
+    if not samples:
+        return None
+    pw = [p for p, _ in samples]
+    ck = [c for _, c in samples]
+    return {"socket_power_w": [min(pw), float(np.median(pw)), max(pw)],
+            "gfx_clock_mhz": [min(ck), float(np.median(ck)), max(ck)], "samples": len(samples)}
+
+
 class LaunchTimer:
     """HIP events around each launch on the current stream."""
 
@@ -901,6 +949,12 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None
 
     # Attention alone (the steps' K/V are in the pages from the runs above).
     attn_ms = region_ms(lambda: [run_attention() for _ in range(reps)], device) / reps
+    power = None
+    if full and page_size == 16 and dtype == torch.float16:
+        power = power_during(run_attention, device)
+        if power:
+            log(f"prefill attention back to back: socket power {power['socket_power_w'][1]:.0f} W "
+                f"(median of {power['samples']} samples), GFX clock {power['gfx_clock_mhz'][1]:.0f} MHz")
     timer = LaunchTimer()   # per-step breakdown (these events add about 5 us a step)
     run(timer)
     torch.cuda.synchronize()
@@ -938,7 +992,8 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None
             "ms_with_append": elapsed * 1e3, "attention_ms": attn_ms, "tflops": tflops,
             "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS, "page_size": page_size,
             "algorithmic_bytes": nbytes, "flop_per_byte": flops / nbytes,
-            "roofline_ms": roof_ms, "roofline_frac": roof_ms / attn_ms, "rope_append": rope,
+            "roofline_ms": roof_ms, "roofline_frac": roof_ms / attn_ms, "power": power,
+            "rope_append": rope,
             "append": append, "cpu_baseline": cpu}
 
 
