@@ -533,6 +533,7 @@ __global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merg
                                                              int64_t o_tok, int64_t o_head,
                                                              int32_t num_qo_heads) {
   constexpr int DPL = D / kWave;
+  typedef float PartVec __attribute__((ext_vector_type(DPL)));
   const int32_t* mg = merges + 4 * blockIdx.x;
   const int seq = mg[0], s0 = mg[1], n = mg[2];
   const int hq = blockIdx.y;
@@ -544,6 +545,10 @@ __global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merg
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
 
+  // Partials are read kBatch at a time, each batch's loads issued together
+  // (one partial at a time waits a memory round trip per partial), and
+  // summed in partition order, so the result does not depend on timing.
+  constexpr int kBatch = 8;
   float o[DPL] = {};
   float wsum = 0.f;
   if (mx > -INFINITY) {
@@ -551,12 +556,23 @@ __global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merg
       const int j = base + lane;
       const float w = j < n ? fast_exp2(part_lse[int64_t(s0 + j) * num_qo_heads + hq] - mx) : 0.f;
       wsum += w;
-      const int cnt = min(kWave, n - base);
-      for (int t = 0; t < cnt; ++t) {   // not unrollable: __shfl is convergent
-        const float wt = __shfl(w, t);
-        const float* src = part_o + (int64_t(s0 + base + t) * num_qo_heads + hq) * D + lane * DPL;
+      const int cnt = min(kWave, n - base);   // uniform
+      for (int t0 = 0; t0 < cnt; t0 += kBatch) {
+        PartVec x[kBatch];
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) o[e] = fmaf(wt, src[e], o[e]);
+        for (int u = 0; u < kBatch; ++u) {
+          const float* src =
+              part_o + (int64_t(s0 + base + t0 + u) * num_qo_heads + hq) * D + lane * DPL;
+          x[u] = t0 + u < cnt ? *reinterpret_cast<const PartVec*>(src) : PartVec{};
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const float wt = __shfl(w, t0 + u);   // every lane: t0 + u < kWave
+          if (t0 + u < cnt) {
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) o[e] = fmaf(wt, x[u][e], o[e]);
+          }
+        }
       }
     }
   }
