@@ -539,32 +539,39 @@ __global__ __launch_bounds__(kWave) void decode_merge_kernel(const int32_t* merg
   const int hq = blockIdx.y;
   const int lane = threadIdx.x;
 
-  float mx = -INFINITY;
-  for (int j = lane; j < n; j += kWave)
+  // Partials are read kBatch at a time, each batch's loads issued together
+  // (one partial at a time waits a memory round trip per partial), and
+  // summed in partition order, so the result does not depend on timing.
+  // The first batch goes out with the first 64 log-sum-exps, before the
+  // maximum they are weighted by is known.
+  constexpr int kBatch = 8;
+  PartVec x[kBatch];
+  auto load_batch = [&](int first, int cnt) {   // partials first .. first + min(cnt, kBatch)
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const float* src = part_o + (int64_t(s0 + first + u) * num_qo_heads + hq) * D + lane * DPL;
+      x[u] = u < cnt ? *reinterpret_cast<const PartVec*>(src) : PartVec{};
+    }
+  };
+  float lse = lane < n ? part_lse[int64_t(s0 + lane) * num_qo_heads + hq] : -INFINITY;
+  load_batch(0, n);
+  float mx = lse;
+  for (int j = lane + kWave; j < n; j += kWave)
     mx = fmaxf(mx, part_lse[int64_t(s0 + j) * num_qo_heads + hq]);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
 
-  // Partials are read kBatch at a time, each batch's loads issued together
-  // (one partial at a time waits a memory round trip per partial), and
-  // summed in partition order, so the result does not depend on timing.
-  constexpr int kBatch = 8;
   float o[DPL] = {};
   float wsum = 0.f;
   if (mx > -INFINITY) {
     for (int base = 0; base < n; base += kWave) {
       const int j = base + lane;
-      const float w = j < n ? fast_exp2(part_lse[int64_t(s0 + j) * num_qo_heads + hq] - mx) : 0.f;
+      if (base > 0) lse = j < n ? part_lse[int64_t(s0 + j) * num_qo_heads + hq] : -INFINITY;
+      const float w = j < n ? fast_exp2(lse - mx) : 0.f;
       wsum += w;
       const int cnt = min(kWave, n - base);   // uniform
       for (int t0 = 0; t0 < cnt; t0 += kBatch) {
-        PartVec x[kBatch];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const float* src =
-              part_o + (int64_t(s0 + base + t0 + u) * num_qo_heads + hq) * D + lane * DPL;
-          x[u] = t0 + u < cnt ? *reinterpret_cast<const PartVec*>(src) : PartVec{};
-        }
+        if (base + t0 > 0) load_batch(base + t0, cnt - t0);
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
           const float wt = __shfl(w, t0 + u);   // every lane: t0 + u < kWave
