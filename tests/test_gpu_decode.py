@@ -129,6 +129,26 @@ def test_decode_split_invariance(device):
     assert max_abs(outs[0][torch.from_numpy(rows).to(device)], want) <= ATOL
 
 
+def test_decode_rows_of_more_than_64_partitions(device):
+    """Rows split into more partitions than a wave has lanes (79 and 65 of
+    256 tokens, and 8 and 9: one batch of partials and one more) merge in
+    more than one round of log-sum-exps, and match the oracle and a plan
+    with 4096-token partitions."""
+    rng = np.random.default_rng(15)
+    kv = np.array([20000, 17, 16400, 2048, 2049, 300], dtype=np.int32)
+    need = (kv + 15) // 16
+    indptr = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    npg = int(indptr[-1]) + 3
+    indices = rng.permutation(npg)[:indptr[-1]].astype(np.int32)
+    pool = random_pool(npg, 1, 8, 16, 128, device, 53)
+    q, out, plan = run_decode(pool, 0, indptr, indices, kv, 32, device, 54, 256)
+    assert plan.info.part_tokens == 256 and plan.info.num_merge > 0
+    want = oracle_decode(pool, 0, indptr, indices, kv, q)
+    assert max_abs(out, want) <= ATOL
+    _, out_long, _ = run_decode(pool, 0, indptr, indices, kv, 32, device, 54, 4096)
+    assert max_abs(out, out_long.float()) <= 1e-3
+
+
 def test_decode_page_permutation_bit_exact(device):
     """Moving pages (and the table with them) does not change one bit."""
     rng = np.random.default_rng(6)
