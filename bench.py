@@ -96,7 +96,7 @@ def power_during(fn, device, seconds: float = 4.0):
                 return
             pw = re.search(r"SOCKET_POWER:\s*(\d+)", out)
             clk = [int(x) for x in re.findall(r"GFX_\d+:\s+CLK:\s*(\d+) MHz", out)]
-            if pw and clk:
+            if pw and clk and not stop.is_set():   # read while the loop still ran
                 samples.append((int(pw.group(1)), float(np.median(clk))))
             stop.wait(0.3)
 
