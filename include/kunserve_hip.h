@@ -150,7 +150,10 @@ int kunserve_hbm_probe(int32_t mode, const void* src_dev, void* dst_dev,
  * i * num_heads + h reads item i's counts_dev[i] slabs at byte offsets
  * slab_offsets_dev[i * max_slabs + j] + h * head_stride_bytes from k_dev and
  * v_dev, and writes the XOR of every 32-bit word it read to sink_dev[i *
- * num_heads + h]. The benchmark times it beside the decode launch. */
+ * num_heads + h]. Counts above max_slabs are read as max_slabs; the
+ * offsets are device data the library cannot check, so the caller keeps
+ * every slab inside both pools. The benchmark times it beside the decode
+ * launch. */
 int kunserve_decode_slab_probe(const void* k_dev, const void* v_dev,
                                const int64_t* slab_offsets_dev,
                                const int32_t* counts_dev, int32_t num_items,

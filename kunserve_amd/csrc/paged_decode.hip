@@ -897,7 +897,7 @@ __global__ __launch_bounds__(kThreads) void decode_slab_probe_kernel(
   __shared__ uint32_t s_x[kWaves];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int item = blockIdx.x / heads, head = blockIdx.x % heads;
-  const int n = counts[item];
+  const int n = min(counts[item], max_slabs);
   const int64_t* o = offs + int64_t(item) * max_slabs;
   const int64_t hoff = int64_t(head) * head_bytes;
   u32x4 acc = {0u, 0u, 0u, 0u};

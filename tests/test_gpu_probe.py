@@ -65,7 +65,8 @@ def test_hbm_probe_copy_is_exact():
 @pytest.mark.parametrize("page_size,head_dim", [(16, 128), (16, 64), (64, 128)])
 def test_decode_slab_probe_reads_the_slabs(page_size, head_dim):
     """The slab probe XORs exactly the words of its items' slabs (K and V,
-    every head) into one word per workgroup; bad arguments are rejected."""
+    every head) into one word per workgroup, reading a count above
+    max_slabs as max_slabs; bad arguments are rejected."""
     from kunserve_amd import KVPool
     dev = torch.device("cuda", 0)
     g = torch.Generator(device=dev)
@@ -74,12 +75,13 @@ def test_decode_slab_probe_reads_the_slabs(page_size, head_dim):
     for t in (pool.k, pool.v):
         t.copy_(torch.randn(t.shape, generator=g, device=dev))
     rng = np.random.default_rng(0)
-    counts = np.array([5, 0, 1, 8], dtype=np.int32)
+    counts = np.array([5, 0, 1, 11], dtype=np.int32)
     max_slabs = 8
     layer = 1
     es = pool.k.element_size()
     pages = np.zeros((4, max_slabs), dtype=np.int64)
-    for i, n in enumerate(counts):
+    used = np.minimum(counts, max_slabs)
+    for i, n in enumerate(used):
         pages[i, :n] = rng.choice(40, size=n, replace=False)
     offs = pages * pool.k.stride(0) * es + layer * pool.k.stride(1) * es
     slab_bytes = page_size * head_dim * es
@@ -94,7 +96,7 @@ def test_decode_slab_probe_reads_the_slabs(page_size, head_dim):
     kw = pool.k.cpu().numpy().view(np.uint32)
     vw = pool.v.cpu().numpy().view(np.uint32)
     want = np.zeros(12, dtype=np.uint32)
-    for i, n in enumerate(counts):
+    for i, n in enumerate(used):
         for h in range(3):
             x = np.uint32(0)
             for p in pages[i, :n]:
