@@ -227,15 +227,14 @@ def slab_ceiling(w, pool, plan, device, launch_ms, reps=5):
     from kunserve_amd import _lib
 
     indptr, indices = w.csr()
-    rec = plan.plan_host[: 4 * plan.info.num_work].reshape(-1, 4)
-    rec = rec[rec[:, 0] >= 0]
+    rec = plan.plan_host[: 4 * plan.info.num_work].reshape(-1, 4)   # padding: seq -1
     shift = int(w.page_size).bit_length() - 1
     max_slabs = max(1, plan.info.part_tokens // w.page_size + 1)
     es = pool.k.element_size()
     base = np.zeros((len(rec), max_slabs), dtype=np.int64)
     counts = np.zeros(len(rec), dtype=np.int32)
     for i, (seq, tb, te, _) in enumerate(rec):
-        if te > tb:
+        if seq >= 0 and te > tb:
             pages = indices[indptr[seq] + (tb >> shift): indptr[seq] + ((te - 1) >> shift) + 1]
             base[i, : len(pages)] = pages.astype(np.int64) * pool.k.stride(0) * es
             counts[i] = len(pages)

@@ -146,11 +146,14 @@ int kunserve_hbm_probe(int32_t mode, const void* src_dev, void* dst_dev,
 /* Access-pattern calibration (no reference counterpart): reads a decode
  * launch's K/V slabs (slab_bytes each: one page's tokens of one head, a
  * multiple of 1 KiB up to 16 KiB) in the partition kernel's workgroup
- * shape, with no page-table lookups and no arithmetic. Workgroup
- * i * num_heads + h reads item i's counts_dev[i] slabs at byte offsets
+ * shape and dispatch order (num_items, a multiple of 8, are the plan's
+ * work records: 8 XCD lanes interleaved, an item's heads on one XCD), with
+ * no page-table lookups and no arithmetic. The workgroup of item i and
+ * head h reads counts_dev[i] slabs at byte offsets
  * slab_offsets_dev[i * max_slabs + j] + h * head_stride_bytes from k_dev and
  * v_dev, and writes the XOR of every 32-bit word it read to sink_dev[i *
- * num_heads + h]. Counts above max_slabs are read as max_slabs; the
+ * num_heads + h]. max_slabs is at most 1026 (the decode's longest
+ * partition in pages); counts above max_slabs are read as max_slabs; the
  * offsets are device data the library cannot check, so the caller keeps
  * every slab inside both pools. The benchmark times it beside the decode
  * launch. */

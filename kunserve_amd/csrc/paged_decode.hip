@@ -693,26 +693,47 @@ extern "C" int kunserve_decode_plan(const int32_t* kv_len_host, int32_t num_seqs
   const int64_t head_groups = num_qo_heads / group;
 
   if (part_tokens == 0) {
-    // Aim for ~8 partitions per CU over the whole grid: the largest
-    // power-of-two partition not above (total tokens x head groups) /
-    // (8 x CUs). Long rows are then split finely enough that the longest
-    // work item is a small fraction of the launch, while short batches
-    // keep whole rows (no merge pass).
+    // The longest power-of-two partition whose longest work item is at most
+    // 3/4 of one CU's share of the launch (a workgroup streams nearly as
+    // fast alone as a CU's share of the device, so an item that long still
+    // ends with the others when it starts first) and that gives every CU
+    // at least 4 workgroups. Longer partitions mean fewer splits, fewer
+    // partials and, once no row is split, no merge launch: the Llama-2-7B
+    // decode (64 rows of lognormal(700) tokens, 32 heads) takes 136.0 us
+    // per layer at 4096 (whole rows) against 138.7 at 2048, 139.0 at 1024
+    // and 140.3 at 512, and the Llama-3-8B GQA and Llama-2-70B layers run
+    // 1.4% and 2.4% faster at 4096 than at 2048.
     int64_t total = 0;
-    for (int32_t b = 0; b < num_seqs; ++b) total += kv_len_host[b];
-    const int64_t per = total * head_groups / (int64_t(std::max(num_cus, 1)) * 8);
+    int32_t max_len = 0;
+    for (int32_t b = 0; b < num_seqs; ++b) {
+      total += kv_len_host[b];
+      max_len = std::max(max_len, kv_len_host[b]);
+    }
+    const int64_t cus = std::max(num_cus, 1);
+    const double share = double(total) * double(head_groups) / double(cus);
+    auto workgroups = [&](int64_t part) {
+      int64_t n = 0;
+      for (int32_t b = 0; b < num_seqs; ++b)
+        n += std::max<int64_t>(1, ceil_div(kv_len_host[b], part));
+      return n * head_groups;
+    };
     part_tokens = kMinPartTokens;
-    while (part_tokens * 2 <= std::min<int64_t>(per, kMaxPartTokens)) part_tokens *= 2;
+    for (int64_t part = kMaxPartTokens; part > kMinPartTokens; part /= 2) {
+      if (double(std::min<int64_t>(part, max_len)) <= 0.75 * share &&
+          workgroups(part) >= 4 * cus) {
+        part_tokens = int32_t(part);
+        break;
+      }
+    }
     // A short launch (under 8 minimum partitions per CU) whose whole rows
     // already give every CU a work item, none longer than two partitions:
     // splitting would at most halve the longest item and add the merge
     // launch, which costs more than that here (single-layer batch of 8
     // rows of U[128, 512] tokens: 10.2 us unsplit against 12.2-13.2 us
     // split at 256). Keep whole rows then.
-    int32_t max_len = 0;
-    for (int32_t b = 0; b < num_seqs; ++b) max_len = std::max(max_len, kv_len_host[b]);
-    if (per < kMinPartTokens && int64_t(num_seqs) * head_groups >= std::max(num_cus, 1) &&
-        max_len <= 2 * part_tokens) {
+    const int64_t per = total * head_groups / (cus * 8);
+    if (part_tokens == kMinPartTokens && per < kMinPartTokens &&
+        int64_t(num_seqs) * head_groups >= cus && max_len <= 2 * part_tokens) {
       while (part_tokens < max_len && part_tokens < kMaxPartTokens) part_tokens *= 2;
     }
   }
@@ -894,25 +915,34 @@ template <int NL>
 __global__ __launch_bounds__(kThreads) void decode_slab_probe_kernel(
     const char* k, const char* v, const int64_t* offs, const int32_t* counts, int max_slabs,
     int64_t head_bytes, int heads, uint32_t* sink) {
+  __shared__ int64_t s_off[kMaxPartPages];
   __shared__ uint32_t s_x[kWaves];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int item = blockIdx.x / heads, head = blockIdx.x % heads;
+  // The decode's dispatch order: an item's heads on one XCD, items of the
+  // 8 XCD lanes interleaved.
+  const int j = int(blockIdx.x) >> 3;
+  const int local = j / heads;
+  const int head = j - local * heads;
+  const int item = 8 * local + (int(blockIdx.x) & 7);
   const int n = min(counts[item], max_slabs);
+  // The item's offsets are staged in LDS, as the decode stages its page ids.
   const int64_t* o = offs + int64_t(item) * max_slabs;
+  for (int i = threadIdx.x; i < n; i += kThreads) s_off[i] = o[i];
+  __syncthreads();
   const int64_t hoff = int64_t(head) * head_bytes;
   u32x4 acc = {0u, 0u, 0u, 0u};
   u32x4 a[2 * NL], b[2 * NL];
   int s = wave;
-  if (s < n) probe_slab<NL>(k, v, o[s] + hoff, lane, a);
+  if (s < n) probe_slab<NL>(k, v, s_off[s] + hoff, lane, a);
   while (s < n) {
     const int s2 = s + kWaves;
-    if (s2 < n) probe_slab<NL>(k, v, o[s2] + hoff, lane, b);
+    if (s2 < n) probe_slab<NL>(k, v, s_off[s2] + hoff, lane, b);
 #pragma unroll
     for (int i = 0; i < 2 * NL; ++i) acc ^= a[i];
     s = s2;
     if (s >= n) break;
     const int s3 = s + kWaves;
-    if (s3 < n) probe_slab<NL>(k, v, o[s3] + hoff, lane, a);
+    if (s3 < n) probe_slab<NL>(k, v, s_off[s3] + hoff, lane, a);
 #pragma unroll
     for (int i = 0; i < 2 * NL; ++i) acc ^= b[i];
     s = s3;
@@ -926,7 +956,7 @@ __global__ __launch_bounds__(kThreads) void decode_slab_probe_kernel(
     uint32_t r = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) r ^= s_x[w];
-    sink[blockIdx.x] = r;
+    sink[item * heads + head] = r;
   }
 }
 
@@ -943,8 +973,9 @@ extern "C" int kunserve_decode_slab_probe(const void* k_dev, const void* v_dev,
   clear_error();
   KSV_CHECK_ARG(k_dev && v_dev && slab_offsets_dev && counts_dev && sink_dev, "null argument");
   KSV_CHECK_ARG(aligned16(k_dev) && aligned16(v_dev), "pools must be 16-byte aligned");
-  KSV_CHECK_ARG(num_items >= 0 && max_slabs > 0 && num_heads > 0 && head_stride_bytes >= 0,
-                "bad item, slab or head count");
+  KSV_CHECK_ARG(num_items >= 0 && num_items % 8 == 0 && max_slabs > 0 &&
+                    max_slabs <= kMaxPartPages && num_heads > 0 && head_stride_bytes >= 0,
+                "bad item (a multiple of 8), slab (at most %d) or head count", kMaxPartPages);
   KSV_CHECK_ARG(slab_bytes > 0 && slab_bytes % 1024 == 0 && slab_bytes / 1024 <= kMaxSlabLoads,
                 "slab_bytes %d must be a multiple of 1024 up to %d", slab_bytes,
                 kMaxSlabLoads * 1024);

@@ -117,11 +117,27 @@ def test_decode_plan_keeps_whole_rows_in_short_launches():
     # a row longer than two minimum partitions: split
     info = _auto_decode_plan(np.r_[w.kv_len, 600], 32, 32)
     assert info.part_tokens == 256 and info.num_merge > 0
-    # the Llama-2-7B and Llama-3-8B GQA workloads keep their partitions
+    # the Llama-2-7B, Llama-3-8B GQA and Llama-2-70B workloads take the
+    # longest partitions: 7B rows are then whole (no merge launch)
     w = workloads.llama2_7b_decode()
-    assert _auto_decode_plan(w.kv_len, 32, 32).part_tokens == 512
+    info = _auto_decode_plan(w.kv_len, 32, 32)
+    assert info.part_tokens == 4096 and info.num_merge == 0
     w = workloads.llama3_8b_gqa_decode()
-    assert _auto_decode_plan(w.kv_len, 32, 8).part_tokens == 2048
+    assert _auto_decode_plan(w.kv_len, 32, 8).part_tokens == 4096
+    w = workloads.kv_remap().decode
+    assert _auto_decode_plan(w.kv_len, 64, 8).part_tokens == 4096
+
+
+def test_decode_plan_automatic_partition_bounds():
+    """The automatic partition keeps the longest item within 3/4 of a CU's
+    share of the launch and gives every CU at least 4 workgroups: one row
+    of 32768 tokens over 32 heads (a CU's share 4096 tokens) is cut into
+    1024-token partitions (1024 workgroups on 256 CUs), and 16 rows of
+    4096 tokens over 32 heads into 2048-token ones (1024 workgroups)."""
+    info = _auto_decode_plan(np.array([32768], dtype=np.int32), 32, 32)
+    assert info.part_tokens == 1024 and info.num_merge == 1
+    info = _auto_decode_plan(np.full(16, 4096, dtype=np.int32), 32, 32)
+    assert info.part_tokens == 2048
 
 
 def test_decode_plan_rejects_bad_arguments():

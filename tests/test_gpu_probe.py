@@ -75,27 +75,27 @@ def test_decode_slab_probe_reads_the_slabs(page_size, head_dim):
     for t in (pool.k, pool.v):
         t.copy_(torch.randn(t.shape, generator=g, device=dev))
     rng = np.random.default_rng(0)
-    counts = np.array([5, 0, 1, 11], dtype=np.int32)
+    counts = np.array([5, 0, 1, 11, 2, 0, 0, 3], dtype=np.int32)   # 8 items: one per XCD lane
     max_slabs = 8
     layer = 1
     es = pool.k.element_size()
-    pages = np.zeros((4, max_slabs), dtype=np.int64)
+    pages = np.zeros((8, max_slabs), dtype=np.int64)
     used = np.minimum(counts, max_slabs)
     for i, n in enumerate(used):
         pages[i, :n] = rng.choice(40, size=n, replace=False)
     offs = pages * pool.k.stride(0) * es + layer * pool.k.stride(1) * es
     slab_bytes = page_size * head_dim * es
-    sink = torch.zeros(4 * 3, dtype=torch.int32, device=dev)
+    sink = torch.zeros(8 * 3, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     offs_dev = torch.from_numpy(offs).to(dev)
     cnt_dev = torch.from_numpy(counts).to(dev)
     _lib.call("kunserve_decode_slab_probe", pool.k.data_ptr(), pool.v.data_ptr(),
-              offs_dev.data_ptr(), cnt_dev.data_ptr(), 4, max_slabs, pool.k.stride(2) * es, 3,
+              offs_dev.data_ptr(), cnt_dev.data_ptr(), 8, max_slabs, pool.k.stride(2) * es, 3,
               slab_bytes, sink.data_ptr(), stream)
     torch.cuda.synchronize()
     kw = pool.k.cpu().numpy().view(np.uint32)
     vw = pool.v.cpu().numpy().view(np.uint32)
-    want = np.zeros(12, dtype=np.uint32)
+    want = np.zeros(24, dtype=np.uint32)
     for i, n in enumerate(used):
         for h in range(3):
             x = np.uint32(0)
@@ -106,6 +106,10 @@ def test_decode_slab_probe_reads_the_slabs(page_size, head_dim):
     assert np.array_equal(sink.cpu().numpy().view(np.uint32), want)
     with pytest.raises(_lib.KunserveError):
         _lib.call("kunserve_decode_slab_probe", pool.k.data_ptr(), pool.v.data_ptr(),
-                  offs_dev.data_ptr(), cnt_dev.data_ptr(), 4, max_slabs, 0, 3, 1000,
+                  offs_dev.data_ptr(), cnt_dev.data_ptr(), 8, max_slabs, 0, 3, 1000,
+                  sink.data_ptr(), stream)
+    with pytest.raises(_lib.KunserveError, match="multiple of 8"):
+        _lib.call("kunserve_decode_slab_probe", pool.k.data_ptr(), pool.v.data_ptr(),
+                  offs_dev.data_ptr(), cnt_dev.data_ptr(), 4, max_slabs, 0, 3, slab_bytes,
                   sink.data_ptr(), stream)
 
