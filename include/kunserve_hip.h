@@ -236,8 +236,11 @@ int64_t kunserve_decode_plan_bound(const int32_t* kv_len_host,
 
 /* Host-side plan, shared by every layer of one step (decode rows only).
  * Splits each sequence into partitions of part_tokens (0 = choose from
- * num_cus so that the grid fills the device), orders the work, and writes
- * it to plan_host (int32, upload it to the device as-is). */
+ * num_cus: the longest power of two in [256, 4096] whose longest work item
+ * is at most 3/4 of one CU's share of the launch and that gives every CU
+ * at least 4 workgroups, or whole rows for a short launch whose rows are
+ * at most two minimum partitions), orders the work, and writes it to
+ * plan_host (int32, upload it to the device as-is). */
 int kunserve_decode_plan(const int32_t* kv_len_host, int32_t num_seqs,
                          int32_t num_qo_heads, int32_t num_kv_heads,
                          int32_t num_cus, int32_t part_tokens,
