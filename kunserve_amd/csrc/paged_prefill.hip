@@ -361,49 +361,48 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   const int kb0 = r * G::kKPitch + 8 * h;
   const VtBases vb = vt_operand_bases(lane);
 
-  auto compute = [&](int buf, int n0) {
-    const T* kt = sK + buf * G::kKHalves + kb0;
-    const T* vt = sVt + buf * G::kVtHalves;
-    // S^T tiles: rows = kv tokens 32*mt + i, columns = query rows.
-    f32x16 st[2];
+  // A tile is two 32-token halves. The score MFMAs of the second half are
+  // issued before the first half's max, and the first half's P.V before the
+  // second half's max, so that with one wave per SIMD the matrix cores have
+  // work while the wave runs each half's softmax.
+  auto half_scores = [&](int buf, int hh) {
+    const T* kt = sK + buf * G::kKHalves + kb0 + 32 * hh * G::kKPitch;
+    f32x16 sv = mfma32(*reinterpret_cast<const V8*>(kt), qf[0], f32x16{});
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      st[mt] = mfma32(*reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch), qf[0], f32x16{});
-#pragma unroll
-      for (int s = 1; s < G::kSteps; ++s) {
-        const V8 ka = *reinterpret_cast<const V8*>(kt + 32 * mt * G::kKPitch + 16 * s);
-        st[mt] = mfma32(ka, qf[s], st[mt]);
-      }
-    }
-    // Lane holds tokens n0 + 32mt + 8(v/4) + 4h + v%4 of query row r.
+    for (int st = 1; st < G::kSteps; ++st)
+      sv = mfma32(*reinterpret_cast<const V8*>(kt + 16 * st), qf[st], sv);
+    return sv;
+  };
+  // Masks (on tiles that need them) and the row max, in log2 units, of half
+  // hh of the tile at n0. Lane (r, h) holds tokens n0 + 32 hh + 8 (v / 4) +
+  // 4 h + v % 4 of query row r; lanes r and r + 32 hold the row's two halves.
+  auto half_max = [&](f32x16& sv, int n0, int hh, bool masked) {
     float mx = -INFINITY;
-    if (n0 + kTileKV - 1 > wave_first_pos || n0 + kTileKV > kvl || any_bad) {
+    if (masked) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int v4 = 0; v4 < 4; ++v4) {
+        // The 4 tokens of a group share one page (page_size >= 4).
+        const int tok0 = n0 + 32 * hh + 8 * v4 + 4 * h;
+        const bool skip = any_bad && tok0 < kv_end && bad_page(tok0);
 #pragma unroll
-        for (int v4 = 0; v4 < 4; ++v4) {
-          // The 4 tokens of a group share one page (page_size >= 4).
-          const int tok0 = n0 + 32 * mt + 8 * v4 + 4 * h;
-          const bool skip = any_bad && tok0 < kv_end && bad_page(tok0);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int v = 4 * v4 + e;
-            const int tok = tok0 + e;
-            if (skip || tok > qpos || tok >= kvl) st[mt][v] = -INFINITY;
-            mx = fmaxf(mx, st[mt][v]);
-          }
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * v4 + e;
+          const int tok = tok0 + e;
+          if (skip || tok > qpos || tok >= kvl) sv[v] = -INFINITY;
+          mx = fmaxf(mx, sv[v]);
         }
+      }
     } else {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, st[mt][v]);
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sv[v]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
-    // Lazy running max: move it only when the tile's max exceeds it by more
-    // than 8 (log2 units). Probabilities then stay <= 2^8, far inside the
-    // fp16 range, and the O rescale is skipped unless some row of the wave
-    // moved.
+    return fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
+  };
+  // Lazy running max: move it only when a half's max exceeds it by more
+  // than 8 (log2 units). Probabilities then stay <= 2^8, far inside the
+  // fp16 range, and the O rescale is skipped unless some row of the wave
+  // moved.
+  auto rescale = [&](float mx) {
     if (__any(mx > m + 8.f)) {
       const float m_new = mx > m + 8.f ? mx : m;
       const float alpha = fast_exp2(m - m_new);
@@ -412,32 +411,46 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
 #pragma unroll
       for (int dt = 0; dt < G::kBlocks; ++dt) o[dt] *= alpha;
     }
-
-    // P^T as B operands: k-step ks covers tokens 16ks + 4h + {0..3} and
-    // 16ks + 8 + 4h + {0..3}, i.e. accumulator entries v = 8(ks%2) + e of tile ks/2.
-    V8 pb[4];
+  };
+  // P^T as B operands: k-step kk covers tokens 16 kk + 4h + {0..3} and
+  // 16 kk + 8 + 4h + {0..3} of the half, i.e. accumulator entries 8 kk + e.
+  auto probs = [&](const f32x16& sv, V8 (&pb)[2]) {
     float ps = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float p = fast_exp2(fmaf(st[mt][v], a.scale_log2, -m));
-        ps += p;
-        pb[2 * mt + (v >> 3)][v & 7] = T(p);
-      }
+    for (int v = 0; v < 16; ++v) {
+      const float p = fast_exp2(fmaf(sv[v], a.scale_log2, -m));
+      ps += p;
+      pb[v >> 3][v & 7] = T(p);
+    }
     lsum += ps;
-
-    // O^T[dims, rows] += V^T[dims, tokens] . P^T[tokens, rows]; the A operand
-    // for k-step ks is tokens 16ks + 4h + {0..3} then 16ks + 8 + 4h + {0..3}.
+  };
+  // O^T[dims, rows] += V^T[dims, tokens] . P^T[tokens, rows] over the half's
+  // k-steps 2 hh and 2 hh + 1 of the V^T tile.
+  auto pv = [&](int buf, int hh, const V8 (&pb)[2]) {
+    const T* vt = sVt + buf * G::kVtHalves;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int kk = 0; kk < 2; ++kk) {
+      const int ks = 2 * hh + kk;
 #pragma unroll
       for (int dt = 0; dt < G::kBlocks; ++dt) {
         const V8 va = *reinterpret_cast<const V8*>(vt + vb.b[vt_operand_base_index(ks, dt)] +
                                                     vt_operand_offset(dt));
-        o[dt] = mfma32(va, pb[ks], o[dt]);
+        o[dt] = mfma32(va, pb[kk], o[dt]);
       }
     }
+  };
+
+  auto compute = [&](int buf, int n0) {
+    const bool masked = n0 + kTileKV - 1 > wave_first_pos || n0 + kTileKV > kvl || any_bad;
+    f32x16 s0 = half_scores(buf, 0);
+    f32x16 s1 = half_scores(buf, 1);
+    rescale(half_max(s0, n0, 0, masked));
+    V8 pb[2];
+    probs(s0, pb);
+    pv(buf, 0, pb);
+    rescale(half_max(s1, n0, 1, masked));
+    probs(s1, pb);
+    pv(buf, 1, pb);
   };
 
   if constexpr (G::kRegSets == 1) {
