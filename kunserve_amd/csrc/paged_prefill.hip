@@ -37,16 +37,20 @@ constexpr int kTileKV = 64;           // kv tokens per iteration
 constexpr int kVtPitch = kTileKV;     // halves per row of the transposed V tile
 constexpr int kXcds = 8;              // MI355X: workgroup i runs on XCD i % 8
 
-// Geometry of the attention kernel for one head_dim. Every wave owns 32
-// query rows (the 32x32 MFMA's columns). Up to head_dim 128 a workgroup is
-// 8 waves, two per SIMD; at 256 it is 4 waves, one per SIMD, since the O
-// accumulators and Q operands of a wave then take 192 registers.
+// Geometry of the attention kernel for one head_dim. Every compute wave
+// owns 32 query rows (the 32x32 MFMA's columns). Up to head_dim 128 a
+// workgroup is 8 waves, two per SIMD, each computing and gathering; at 256
+// it is 4 compute waves, one per SIMD, since the O accumulators and Q
+// operands of a wave then take 192 registers, and 4 loader waves, one per
+// SIMD, that only gather K/V tiles into LDS.
 template <int D>
 struct Geom {
   static_assert(D == 64 || D == 128 || D == 256, "prefill head_dim is 64, 128 or 256");
-  static constexpr int kWaves = D <= 128 ? 8 : 4;
+  static constexpr int kComputeWaves = D <= 128 ? 8 : 4;
+  static constexpr int kLoadWaves = D <= 128 ? 0 : 4;
+  static constexpr int kWaves = kComputeWaves + kLoadWaves;
   static constexpr int kThreads = kWaves * kWave;
-  static constexpr int kTileQ = 32 * kWaves;   // query rows per workgroup
+  static constexpr int kTileQ = 32 * kComputeWaves;   // query rows per workgroup
   static constexpr int kSteps = D / 16;        // 16-dim k-steps of S = K.Q^T
   static constexpr int kBlocks = D / 32;       // 32-dim blocks of O
   static constexpr int kKPitch = D + 8;        // halves per K row
@@ -54,7 +58,8 @@ struct Geom {
   static constexpr int kVtHalves = D * kVtPitch;
   // Gather units (4 consecutive tokens x one 16-byte chunk of K or V) per
   // lane of a gathering wave: 64 and 128: one (waves 0-1 / 0-3 gather V,
-  // 2-3 / 4-7 gather K); 256: four (every wave two chunks of V and two of K).
+  // 2-3 / 4-7 gather K); 256: four (every loader wave two chunks of V and
+  // two of K).
   static constexpr int kUnits = D == 256 ? 4 : 1;
   // Gather register sets: two (the tile after next in flight while the next
   // waits to be stashed) up to 128; one at 256, whose register file holds
@@ -249,18 +254,6 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   const int kv_end = min(prefix + min(q0 + G::kTileQ, q_len), kv_hi);   // exclusive
   const int ntiles = (kv_end + kTileKV - 1) / kTileKV;   // tiles [kv_lo / kTileKV, ntiles)
   const int pg_lo = kv_lo >> a.page_shift;   // first staged page
-  // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
-  // Issued before the page-id staging, so that both loads' latencies
-  // overlap, and with no branch: a row past q_len reads the sequence's
-  // first row instead (its scores stay in its own lane column, and it
-  // writes no output).
-  V8 qf[G::kSteps];
-  {
-    const f16* qp = a.q + int64_t(qt + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
-#pragma unroll
-    for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
-  }
-
   // Stage (or, for rows with too many pages, only scan) the page ids of
   // [kv_lo, kv_end). Whether any of them is outside the pool is voted per
   // wave: only then do the scores need a per-page mask, which drops the
@@ -313,7 +306,7 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   const bool stashes = kGatherWaves == G::kWaves || wave < kGatherWaves;
   const int gw = wave % kGatherWaves;
   const bool gather_v = D == 256 || gw < kGatherWaves / 2;   // the first unit's tensor
-  const GatherLane gl = gather_lane<D>(D == 256 ? wave : gw % (kGatherWaves / 2), lane);
+  const GatherLane gl = gather_lane<D>(D == 256 ? wave - G::kComputeWaves : gw % (kGatherWaves / 2), lane);
   const int ld_t = 16 * gl.g + 8 * gl.a + 4 * gl.h;
   const int ld_c = 8 * gl.c;
   // Unit u: tensor (V for the first half at 256), chunk gl.c + 16 (u & 1) at 256.
@@ -354,6 +347,17 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
               rg.x[u][i];
       }
     }
+  };
+
+  // Q as the B operand of S^T = K.Q^T: step s covers dims 16s + 8h .. +8.
+  // Loaded with no branch: a row past q_len reads the sequence's first row
+  // instead (its scores stay in its own lane column, and it writes no
+  // output).
+  V8 qf[G::kSteps];
+  auto qf_load = [&]() {
+    const f16* qp = a.q + int64_t(qt + (row_ok ? qrow : 0)) * a.q_tok + int64_t(hq) * a.q_head;
+#pragma unroll
+    for (int s = 0; s < G::kSteps; ++s) qf[s] = load_v8<T>(qp + 16 * s + 8 * h);
   };
 
   // Per-lane LDS bases; each operand read adds a compile-time offset.
@@ -453,28 +457,42 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
     pv(buf, 1, pb);
   };
 
-  if constexpr (G::kRegSets == 1) {
-    // Tile it is computed from LDS buffer it % 2 while tile it + 1 is
-    // fetched into the one register set and stashed after the math.
-    Regs ra;
-    read_ids(kv_lo);
-    fetch(ra);
-    stash(0, ra);
-    read_ids(kv_lo + kTileKV);
-    __syncthreads();
-    for (int it = kv_lo / kTileKV; it < ntiles; ++it) {
+  if constexpr (G::kLoadWaves > 0) {
+    // Loader waves gather tile it + 1 into the LDS buffers tile it - 1 left
+    // while the compute waves run tile it, and fetch tile it + 2 into their
+    // one register set; one barrier per tile.
+    const int t_first = kv_lo / kTileKV;
+    if (wave >= G::kComputeWaves) {
+      Regs ra;
+      read_ids(kv_lo);
+      fetch(ra);
+      stash(0, ra);
+      read_ids(kv_lo + kTileKV);
+      fetch(ra);   // tile t_first + 1 (past the end: in-bounds reads, never stashed)
+      read_ids(kv_lo + 2 * kTileKV);
+      __syncthreads();   // tile t_first published
+      for (int it = t_first; it < ntiles; ++it) {
+        // Buffer (it + 1) % 2 was last read for tile it - 1, before the
+        // previous barrier.
+        if (it + 1 < ntiles) stash((it - t_first + 1) & 1, ra);
+        fetch(ra);   // tile it + 2
+        read_ids((it + 3) * kTileKV);
+        __syncthreads();
+      }
+      return;
+    }
+    qf_load();
+    __syncthreads();   // tile t_first published
+    for (int it = t_first; it < ntiles; ++it) {
       const int n0 = it * kTileKV;
-      const int buf = (it - kv_lo / kTileKV) & 1;
-      if (it + 1 < ntiles) fetch(ra);
-      if (wave_active && n0 <= wave_last_pos) compute(buf, n0);
-      if (it + 1 < ntiles) stash(buf ^ 1, ra);   // buffer buf ^ 1 was last read before the previous barrier
-      read_ids(n0 + 2 * kTileKV);
+      if (wave_active && n0 <= wave_last_pos) compute((it - t_first) & 1, n0);
       __syncthreads();
     }
   } else {
   // Tile it is computed from LDS buffer it % 2 while tile it + 1 sits in
   // registers (loads issued one iteration earlier) and tile it + 2 is being
   // fetched into the other register set.
+  qf_load();
   Regs ra, rb;
   read_ids(kv_lo);
   fetch(ra);
