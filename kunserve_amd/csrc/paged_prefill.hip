@@ -7,13 +7,15 @@
 // Attention: flash-attention style on fp16 or bf16 MFMA
 // (v_mfma_f32_32x32x16_f16 / _bf16, gfx950), fp32 accumulation and online
 // softmax; kernels are templates over the element type.
-//  * Workgroup = 8 waves = 256 query rows of one (sequence, q head); each
-//    wave owns 32 rows. Two waves share a SIMD (waves w and w + 4).
-//  * K/V tiles of 64 tokens are gathered from pages into double-buffered
-//    LDS: K row-major, V transposed (one row per dim), so that both
-//    operands are 16-byte reads. The gather of the tile after next is
-//    issued before the current tile's math (two register sets), with its
-//    page position looked up one iteration earlier; one barrier per tile.
+//  * Every compute wave owns 32 query rows of one (sequence, q head).
+//    Loader waves gather 64-token K/V tiles from the pages into LDS: K
+//    row-major, V transposed (one row per dim), so that both operands are
+//    16-byte reads; page positions are looked up one tile ahead.
+//  * head_dim 64 and 128 (paged_prefill_ws_kernel): 8 compute waves (256
+//    rows, two per SIMD) and 4 loader waves; a ring of 2 K and 3 V buffers.
+//  * head_dim 256 (paged_prefill_kernel): 4 compute waves (128 rows, one
+//    per SIMD) and 4 loader waves; 2 K and 2 V buffers, one barrier per
+//    tile; each tile's two 32-token halves run as a pipeline.
 //  * S^T = K.Q^T is computed so that the accumulator layout (one query row
 //    per lane column) is directly the B operand of O^T = V^T.P^T: the
 //    probabilities never leave registers.
@@ -62,8 +64,9 @@ struct Geom {
   // two of K).
   static constexpr int kUnits = D == 256 ? 4 : 1;
   // Gather register sets: two (the tile after next in flight while the next
-  // waits to be stashed) up to 128; one at 256, whose register file holds
-  // no second set, and whose tiles take twice the math to cover the loads.
+  // waits to be stashed) up to 128; one at 256, where the loader waves
+  // fetch tile it + 2 as soon as tile it + 1 has left the registers, a whole
+  // tile of math (twice that of 128) ahead of its stash.
   static constexpr int kRegSets = D <= 128 ? 2 : 1;
 };
 
@@ -295,8 +298,8 @@ __global__ __launch_bounds__(Geom<D>::kThreads) void paged_prefill_kernel(Prefil
   // while tile n is computed and tile n + 1 waits to be parked in LDS. One
   // tile's loads take about one HBM round trip, longer than a tile's math.
   // Gather roles (Geom::kUnits): at head_dim 64 waves 0-1 gather V and 2-3
-  // K; at 128 waves 0-3 V and 4-7 K; at 256 every wave both, two chunks of
-  // each. The tile position of a gather is looked up one iteration ahead
+  // K; at 128 waves 0-3 V and 4-7 K; at 256 every loader wave both, two
+  // chunks of each. The tile position of a gather is looked up one iteration ahead
   // (at), so no lookup latency sits in front of the loads. Every wave
   // issues its loads unconditionally (at 64, waves 4-7 repeat those of
   // waves 0-3, which the CU's cache serves, and do not stash them): a
