@@ -14,7 +14,8 @@ utilisation of the fp16 dense peak (and `prefill_page256`, the same
 workload on 256-token pages, the reference's default block size, and
 `bf16_prefill_page256` on a bf16 pool of 256-token pages, both reference
 defaults; `prefill_head_dim64` and `prefill_head_dim256`, the same rows and
-heads at head_dim 64 and 256, attention only), beside `mfma_ceiling`, the
+heads at head_dim 64 and 256, and `prefill_gqa8`, the same rows with
+Llama-3-8B's 32 query / 8 KV heads, attention only), beside `mfma_ceiling`, the
 rate the part sustains on fp16 MFMAs with random and with constant operands;
 `gqa_decode` — Llama-3-8B GQA decode (32/8 heads, batch 128, contexts
 U[1024, 8192]) as HBM bandwidth; `bf16_decode` — the headline decode on a
@@ -816,18 +817,24 @@ def cpu_decode_sample(w, pool, layer, q, rows, budget_s: float) -> dict:
 # ----------------------------------------------------------------- prefill
 
 
-def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None):
+def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None,
+                  num_kv_heads=None):
     """The chunked-prefill workload's 8 steps. head_dim (64 or 256) runs the
-    same rows, pages and heads at another head size: attention only."""
+    same rows, pages and heads at another head size, and num_kv_heads (8:
+    Llama-3-8B's 32 query / 8 KV heads) the same rows with grouped KV
+    heads: attention only."""
     import dataclasses
 
     import kunserve_amd as ks
     from kunserve_amd import workloads
 
     w = workloads.chunked_prefill(page_size=page_size)
-    full = head_dim is None
-    if not full:
+    full = head_dim is None and num_kv_heads is None
+    if head_dim is not None:
         w = dataclasses.replace(w, head_dim=head_dim, name=f"{w.name} head_dim{head_dim}")
+    if num_kv_heads is not None:
+        w = dataclasses.replace(w, num_kv_heads=num_kv_heads,
+                                name=f"{w.name} {w.num_qo_heads}q/{num_kv_heads}kv heads")
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed)
     pool = ks.KVPool.allocate(w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim, device,
@@ -974,7 +981,8 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None
         nbytes += 2 * T * w.num_qo_heads * w.head_dim * elem
         nbytes += int(((kv + w.page_size - 1) // w.page_size).sum()) * 4
     roof_ms = max(flops / (FP16_MFMA_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
-    log(f"prefill ({name}, page {page_size}, head_dim {w.head_dim}): {len(steps)} chunk steps, "
+    log(f"prefill ({name}, page {page_size}, head_dim {w.head_dim}, heads {w.num_qo_heads}/"
+        f"{w.num_kv_heads}): {len(steps)} chunk steps, "
         f"{elapsed * 1e3:.3f} ms with "
         f"append; attention {attn_ms:.3f} ms = {tflops:.1f} TFLOP/s "
         f"({tflops / FP16_MFMA_PEAK_TFLOPS * 100:.1f}% of the {name} MFMA peak)")
@@ -987,6 +995,7 @@ def bench_prefill(args, device, page_size=16, dtype=torch.float16, head_dim=None
         f"{FP16_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):.0f}; roofline time "
         f"{roof_ms:.3f} ms = {roof_ms / attn_ms * 100:.1f}% of the measured")
     return {"workload": w.name, "dtype": name, "head_dim": w.head_dim,
+            "num_qo_heads": w.num_qo_heads, "num_kv_heads": w.num_kv_heads,
             "causal_tflop": flops / 1e12, "steps": len(steps),
             "ms_with_append": elapsed * 1e3, "attention_ms": attn_ms, "tflops": tflops,
             "mfma_util": tflops / FP16_MFMA_PEAK_TFLOPS, "page_size": page_size,
@@ -1198,8 +1207,9 @@ def main():
         print(json.dumps({"mfma_ceiling": mfma_ceiling(device)}))
         return
     if args.only == "prefillhd":
-        print(json.dumps({f"prefill_head_dim{hd}": bench_prefill(args, device, head_dim=hd)
-                          for hd in (64, 256)}))
+        legs = {f"prefill_head_dim{hd}": bench_prefill(args, device, head_dim=hd) for hd in (64, 256)}
+        legs["prefill_gqa8"] = bench_prefill(args, device, num_kv_heads=8)
+        print(json.dumps(legs))
         return
     if args.only == "prefill256":
         print(json.dumps({"prefill_page256": bench_prefill(args, device, page_size=256)}))
@@ -1239,7 +1249,7 @@ def main():
     torch.cuda.empty_cache()
     prefill = prefill256 = prefill_bf16 = gqa = bf16 = bf16_256 = remap = pmm = swp = None
     ceiling = single = mixed = None
-    prefill_hd = {"prefill_head_dim64": None, "prefill_head_dim256": None}
+    prefill_hd = {"prefill_head_dim64": None, "prefill_head_dim256": None, "prefill_gqa8": None}
     if args.only is None:
         single = bench_single_layer(args, device)
         torch.cuda.empty_cache()
@@ -1261,6 +1271,11 @@ def main():
                 k: r[k] for k in ("workload", "head_dim", "causal_tflop", "attention_ms", "tflops",
                                   "mfma_util")}
             torch.cuda.empty_cache()
+        r = bench_prefill(args, device, num_kv_heads=8)
+        prefill_hd["prefill_gqa8"] = {
+            k: r[k] for k in ("workload", "num_qo_heads", "num_kv_heads", "causal_tflop",
+                              "attention_ms", "tflops", "mfma_util", "flop_per_byte")}
+        torch.cuda.empty_cache()
         gqa = bench_gqa(args, device)
         torch.cuda.empty_cache()
         bf16 = bench_bf16_decode(args, device)
