@@ -434,6 +434,7 @@ def bench_gqa(args, device):
     log(f"gqa decode: {w.name}: per launch {res['launch_ms'] * 1e3:.1f} us = "
         f"{res['achieved']:.1f} GB/s ({res['achieved'] / HBM_PEAK_GBS * 100:.1f}% of HBM peak), "
         f"part_tokens {res['plan'].info.part_tokens}, group {res['plan'].info.group_size}")
+    pattern = slab_ceiling(w, pool, res["plan"], device, res["launch_ms"], reps=20)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_decode_sample(w, pool, 0, res["qs"][0], np.arange(0, w.batch, 8),
@@ -441,7 +442,7 @@ def bench_gqa(args, device):
         log(f"gqa decode cpu baseline: {cpu['value']:.3f} GB/s ({cpu['sample']})")
     return {"workload": w.name, "launch_us": res["launch_ms"] * 1e3, "gbs": res["achieved"],
             "hbm_frac": res["achieved"] / HBM_PEAK_GBS, "bytes_per_launch": res["bytes_per_layer"],
-            "cpu_baseline": cpu}
+            "access_pattern": pattern, "cpu_baseline": cpu}
 
 
 def bench_bf16_decode(args, device, page_size=16):
